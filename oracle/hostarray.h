@@ -40,9 +40,9 @@ enum {
     OR_OP_COSH = 17, OR_OP_TANH = 18, OR_OP_SIN = 19, OR_OP_COS = 20,
     OR_OP_TAN = 21, OR_OP_ABS = 22, OR_OP_NEG = 23, OR_OP_CEIL = 26,
     OR_OP_FLOOR = 27, OR_OP_ROUND = 28,
-    OR_OP_REDUCE_SUM = 36, OR_OP_REDUCE_MEAN = 37, OR_OP_REDUCE_MAX = 38,
-    OR_OP_REDUCE_MIN = 39,
-    OR_OP_ARG_MAX = 43, OR_OP_ARG_MIN = 44
+    OR_OP_REDUCE_SUM = 35, OR_OP_REDUCE_MEAN = 36, OR_OP_REDUCE_MAX = 37,
+    OR_OP_REDUCE_MIN = 38,
+    OR_OP_ARG_MAX = 42, OR_OP_ARG_MIN = 43
 };
 
 /* Status codes returned by every oracle entry point. */

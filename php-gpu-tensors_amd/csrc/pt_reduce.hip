@@ -1,0 +1,1326 @@
+// Axis reductions (sum/mean/max/min/prod, argmax/argmin, var/std) and the
+// fused row softmax / layerNorm kernels for gfx950.
+//
+// Layout classes (chosen on the host from shape/strides/axis):
+//   rows    : the reduced axis has stride 1 and the other axes collapse to a
+//             single row index with pitch `ld` -> one wave64 per row,
+//             16-byte vector loads (global_load_dwordx4), DPP/shuffle
+//             wave reduction, no LDS.  This is the HBM-roofline path.
+//   columns : contiguous input reduced over a non-last axis -> (outer, n,
+//             inner), lanes walk `inner` (coalesced), LDS combine over n.
+//   strided : anything else -> one workgroup per output with full stride
+//             decode (correct for every view, not a fast path).
+//   global  : all elements of a contiguous input -> per-workgroup partials
+//             in stream-ordered scratch, then one finishing workgroup.
+//
+// Semantics follow the reference: reduction_ops.cu:148-311 for op/dtype
+// rules, reduction_ops.cuh:319-401 for arg reductions, :86-112 (Welford)
+// for var/std, cuda_array_ce.c:1942-2001 (softmax) and :2215-2339
+// (layerNorm).  max/min skip NaN like HostArray (contiguous_array_ce.c:
+// 1241-1242).
+#include "pt_common.h"
+
+#include <math.h>
+
+namespace pt {
+
+enum RedOp { R_SUM = 0, R_MEAN, R_MAX, R_MIN, R_PROD, R_ARGMAX, R_ARGMIN, R_VAR };
+
+// ------------------------------------------------------------------ traits
+// Storage type S, compute type C, 16-byte vector width V.
+template <int DT> struct RT;
+template <> struct RT<PT_FLOAT32> {
+    using S = float; using C = float; static constexpr int V = 4;
+    __device__ static C cv(S s) { return s; }
+};
+template <> struct RT<PT_FLOAT64> {
+    using S = double; using C = double; static constexpr int V = 2;
+    __device__ static C cv(S s) { return s; }
+};
+template <> struct RT<PT_BFLOAT16> {
+    using S = uint16_t; using C = float; static constexpr int V = 8;
+    __device__ static C cv(S s) { return bf16_to_float(s); }
+};
+template <> struct RT<PT_FLOAT16> {
+    using S = uint16_t; using C = float; static constexpr int V = 8;
+    __device__ static C cv(S s) { return f16_to_float(s); }
+};
+
+template <int DT, int V>
+__device__ __forceinline__ void load_chunk(const typename RT<DT>::S *p, typename RT<DT>::C (&v)[V])
+{
+    using S = typename RT<DT>::S;
+    if constexpr (V * sizeof(S) == 16) {
+        union { uint4 raw; S s[V]; } u;
+        u.raw = *(const uint4 *)p;
+#pragma unroll
+        for (int i = 0; i < V; i++) v[i] = RT<DT>::cv(u.s[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; i++) v[i] = RT<DT>::cv(p[i]);
+    }
+}
+
+template <typename C> __device__ __forceinline__ C neg_inf();
+template <> __device__ __forceinline__ float neg_inf<float>() { return -INFINITY; }
+template <> __device__ __forceinline__ double neg_inf<double>() { return -INFINITY; }
+
+__device__ __forceinline__ float fmax_c(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double fmax_c(double a, double b) { return fmax(a, b); }
+__device__ __forceinline__ float fmin_c(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ double fmin_c(double a, double b) { return fmin(a, b); }
+__device__ __forceinline__ float exp_c(float a) { return expf(a); }
+__device__ __forceinline__ double exp_c(double a) { return exp(a); }
+__device__ __forceinline__ float sqrt_c(float a) { return sqrtf(a); }
+__device__ __forceinline__ double sqrt_c(double a) { return sqrt(a); }
+
+// Moments state for var/std (Chan et al. parallel combination of Welford
+// states, reduction_ops.cuh:97-112).
+struct Mom {
+    double n, mean, m2;
+};
+
+__device__ __forceinline__ Mom mom_combine(Mom a, Mom b)
+{
+    if (a.n == 0) return b;
+    if (b.n == 0) return a;
+    double n = a.n + b.n;
+    double delta = b.mean - a.mean;
+    Mom r;
+    r.n = n;
+    r.mean = a.mean + delta * (b.n / n);
+    r.m2 = a.m2 + b.m2 + delta * delta * (a.n * b.n / n);
+    return r;
+}
+
+__device__ __forceinline__ Mom mom_shfl(Mom m, int lane_mask)
+{
+    Mom o;
+    o.n = __shfl_xor(m.n, lane_mask, PT_WAVE);
+    o.mean = __shfl_xor(m.mean, lane_mask, PT_WAVE);
+    o.m2 = __shfl_xor(m.m2, lane_mask, PT_WAVE);
+    return o;
+}
+
+// Per-lane accumulator for one reduction op over compute type C.
+template <typename C, int OP> struct Acc;
+
+template <typename C> struct Acc<C, R_SUM> {
+    C s = 0;
+    __device__ void add(C v, int) { s = s + v; }
+    __device__ void merge_shfl(int m) { s = s + __shfl_xor(s, m, PT_WAVE); }
+    __device__ void merge(const Acc &o) { s = s + o.s; }
+};
+template <typename C> struct Acc<C, R_MEAN> : Acc<C, R_SUM> {};
+template <typename C> struct Acc<C, R_PROD> {
+    C s = 1;
+    __device__ void add(C v, int) { s = s * v; }
+    __device__ void merge_shfl(int m) { s = s * __shfl_xor(s, m, PT_WAVE); }
+    __device__ void merge(const Acc &o) { s = s * o.s; }
+};
+template <typename C> struct Acc<C, R_MAX> {
+    C s = neg_inf<C>();
+    __device__ void add(C v, int) { s = fmax_c(s, v); }
+    __device__ void merge_shfl(int m) { s = fmax_c(s, __shfl_xor(s, m, PT_WAVE)); }
+    __device__ void merge(const Acc &o) { s = fmax_c(s, o.s); }
+};
+template <typename C> struct Acc<C, R_MIN> {
+    C s = -neg_inf<C>();
+    __device__ void add(C v, int) { s = fmin_c(s, v); }
+    __device__ void merge_shfl(int m) { s = fmin_c(s, __shfl_xor(s, m, PT_WAVE)); }
+    __device__ void merge(const Acc &o) { s = fmin_c(s, o.s); }
+};
+// Arg reductions: elements arrive in increasing index order per lane, so a
+// strict comparison keeps the lowest index; merges break ties by index.
+// NaN compares false and is never taken; identity is (+-inf, 0).
+template <typename C, bool MAXIMIZE> struct ArgAcc {
+    C v = MAXIMIZE ? neg_inf<C>() : -neg_inf<C>();
+    int i = 0;
+    __device__ void add(C x, int idx)
+    {
+        if (MAXIMIZE ? x > v : x < v) { v = x; i = idx; }
+    }
+    __device__ void merge(const ArgAcc &o)
+    {
+        if ((MAXIMIZE ? o.v > v : o.v < v) || (o.v == v && o.i < i)) { v = o.v; i = o.i; }
+    }
+    __device__ void merge_shfl(int m)
+    {
+        ArgAcc o;
+        o.v = __shfl_xor(v, m, PT_WAVE);
+        o.i = __shfl_xor(i, m, PT_WAVE);
+        merge(o);
+    }
+};
+template <typename C> struct Acc<C, R_ARGMAX> : ArgAcc<C, true> {};
+template <typename C> struct Acc<C, R_ARGMIN> : ArgAcc<C, false> {};
+template <typename C> struct Acc<C, R_VAR> {
+    Mom m = {0, 0, 0};
+    C cn = 0, cmean = 0, cm2 = 0;  // running per-lane state in compute type
+    __device__ void add(C v, int)
+    {
+        // single-element Welford step; welford_single seeds m2 with v - v so
+        // that infinities poison the result (reduction_ops.cuh:86-90)
+        C n1 = cn + 1;
+        C delta = v - cmean;
+        cmean = cmean + delta / n1;
+        cm2 = cm2 + (v - v) + delta * (v - cmean);
+        cn = n1;
+    }
+    __device__ Mom lane_state() const { return Mom{(double)cn, (double)cmean, (double)cm2}; }
+};
+
+template <typename C, int OP>
+__device__ __forceinline__ void wave_merge(Acc<C, OP> &a)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) a.merge_shfl(m);
+}
+
+// Chunk-level variance update: V elements at once (exact two-pass on the
+// registers of the chunk, then a Chan combine), one division per chunk.
+template <typename C, int V>
+__device__ __forceinline__ void var_add_chunk(Acc<C, R_VAR> &a, const C (&v)[V], int valid)
+{
+    if (valid == V) {
+        C s = 0;
+#pragma unroll
+        for (int k = 0; k < V; k++) s = s + v[k];
+        C mb = s / (C)V;
+        C m2b = 0;
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            C d = v[k] - mb;
+            m2b = m2b + d * d;
+        }
+        if (a.cn == 0) {
+            a.cn = (C)V; a.cmean = mb; a.cm2 = m2b;
+        } else {
+            C n = a.cn + (C)V;
+            C delta = mb - a.cmean;
+            C r = (C)V / n;
+            a.cmean = a.cmean + delta * r;
+            a.cm2 = a.cm2 + m2b + delta * delta * a.cn * r;
+            a.cn = n;
+        }
+    } else {
+        for (int k = 0; k < valid; k++) a.add(v[k], 0);
+    }
+}
+
+// ------------------------------------------------------ output conversion
+template <typename C>
+__device__ __forceinline__ void store_out(void *out, int out_dt, size_t i, C v)
+{
+    if (out_dt == PT_FLOAT32) ((float *)out)[i] = (float)v;
+    else ((double *)out)[i] = (double)v;
+}
+
+// ============================================================ row kernels
+// One wave64 per row; `rows_per_block` = blockDim.x / 64.  No LDS, no
+// block barrier: waves retire independently.
+template <int DT, int OP, int VEC>
+__global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin, size_t rows,
+                                                    int n, size_t ld, void *__restrict__ out,
+                                                    int out_dt, int correction, int take_sqrt)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const S *x = (const S *)xin + row * ld;
+    Acc<C, OP> acc;
+    constexpr int STEP = 64 * VEC;
+    int i = lane * VEC;
+    // main loop: 4 chunks in flight per lane
+    for (; i + 3 * STEP + VEC <= n; i += 4 * STEP) {
+        C v[4][VEC];
+#pragma unroll
+        for (int u = 0; u < 4; u++) load_chunk<DT, VEC>(x + i + u * STEP, v[u]);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if constexpr (OP == R_VAR) {
+                var_add_chunk<C, VEC>(acc, v[u], VEC);
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; k++) acc.add(v[u][k], i + u * STEP + k);
+            }
+        }
+    }
+    for (; i < n; i += STEP) {
+        C v[VEC];
+        int valid = n - i < VEC ? n - i : VEC;
+        if (valid == VEC) {
+            load_chunk<DT, VEC>(x + i, v);
+        } else {
+            for (int k = 0; k < VEC; k++) v[k] = k < valid ? RT<DT>::cv(x[i + k]) : (C)0;
+        }
+        if constexpr (OP == R_VAR) {
+            var_add_chunk<C, VEC>(acc, v, valid);
+        } else {
+            for (int k = 0; k < valid; k++) acc.add(v[k], i + k);
+        }
+    }
+    if constexpr (OP == R_VAR) {
+        Mom m = acc.lane_state();
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) m = mom_combine(m, mom_shfl(m, s));
+        if (lane == 0) {
+            double var = m.m2 / (double)(n - correction);
+            store_out(out, out_dt, row, take_sqrt ? sqrt(var) : var);
+        }
+    } else {
+        wave_merge(acc);
+        if (lane == 0) {
+            if constexpr (OP == R_ARGMAX || OP == R_ARGMIN) {
+                ((int32_t *)out)[row] = acc.i;
+            } else if constexpr (OP == R_MEAN) {
+                store_out(out, out_dt, row, acc.s / (C)n);
+            } else {
+                store_out(out, out_dt, row, acc.s);
+            }
+        }
+    }
+}
+
+// Fused softmax over register-resident rows: NCH chunks of VEC elements per
+// lane cover the row (n <= 64 * VEC * NCH).  One HBM read, one write.
+// y = exp(x - max) / sum(exp(x - max)): true division as the composite's
+// OP_DIV (cuda_array_ce.c:1995).
+template <int DT, int VEC, int NCH, typename OS>
+__global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xin, size_t rows,
+                                                     int n, size_t ld, OS *__restrict__ out)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const S *x = (const S *)xin + row * ld;
+    OS *y = out + row * (size_t)n;
+    C v[NCH][VEC];
+    C m = neg_inf<C>();
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+        if (i + VEC <= n) {
+            load_chunk<DT, VEC>(x + i, v[c]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; k++) v[c][k] = i + k < n ? RT<DT>::cv(x[i + k]) : neg_inf<C>();
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) m = fmax_c(m, __shfl_xor(m, s, PT_WAVE));
+    C sum = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            C e = i + k < n ? exp_c(v[c][k] - m) : (C)0;
+            v[c][k] = e;
+            sum = sum + e;
+        }
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) sum = sum + __shfl_xor(sum, s, PT_WAVE);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+        if (i + VEC <= n) {
+            OS r[VEC];
+#pragma unroll
+            for (int k = 0; k < VEC; k++) r[k] = (OS)(v[c][k] / sum);
+            if constexpr (VEC * sizeof(OS) == 16) {
+                *(uint4 *)(y + i) = *(const uint4 *)r;
+            } else if constexpr (VEC * sizeof(OS) == 32) {
+                ((uint4 *)(y + i))[0] = ((const uint4 *)r)[0];
+                ((uint4 *)(y + i))[1] = ((const uint4 *)r)[1];
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; k++) y[i + k] = r[k];
+            }
+        } else {
+            for (int k = 0; k < VEC; k++)
+                if (i + k < n) y[i + k] = (OS)(v[c][k] / sum);
+        }
+    }
+}
+
+// Fused layerNorm over register-resident rows (cuda_array_ce.c:2295-2323):
+// mean, centered, biased variance of the centered values, eps inside the
+// sqrt, true division, then gamma and beta.
+template <int DT, int VEC, int NCH, typename CT>
+__global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ xin, size_t rows,
+                                                       int n, CT eps, const CT *__restrict__ gamma,
+                                                       const CT *__restrict__ beta,
+                                                       CT *__restrict__ out)
+{
+    using S = typename RT<DT>::S;
+    const int lane = threadIdx.x & 63;
+    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const S *x = (const S *)xin + row * (size_t)n;
+    CT *y = out + row * (size_t)n;
+    CT v[NCH][VEC];
+    CT s = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+        if (i + VEC <= n) {
+            typename RT<DT>::C t[VEC];
+            load_chunk<DT, VEC>(x + i, t);
+#pragma unroll
+            for (int k = 0; k < VEC; k++) v[c][k] = (CT)t[k];
+        } else {
+#pragma unroll
+            for (int k = 0; k < VEC; k++) v[c][k] = i + k < n ? (CT)RT<DT>::cv(x[i + k]) : (CT)0;
+        }
+#pragma unroll
+        for (int k = 0; k < VEC; k++) s = s + v[c][k];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m, PT_WAVE);
+    const CT mean = s / (CT)n;
+    CT q = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            CT d = i + k < n ? v[c][k] - mean : (CT)0;
+            v[c][k] = d;
+            q = q + d * d;
+        }
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) q = q + __shfl_xor(q, m, PT_WAVE);
+    const CT dev = sqrt_c(q / (CT)n + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        int i = (c * 64 + lane) * VEC;
+        CT r[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            CT t = v[c][k] / dev;
+            if (gamma && i + k < n) t = t * gamma[i + k];
+            if (beta && i + k < n) t = t + beta[i + k];
+            r[k] = t;
+        }
+        if (i + VEC <= n) {
+            if constexpr (VEC * sizeof(CT) == 16) {
+                *(uint4 *)(y + i) = *(const uint4 *)r;
+            } else if constexpr (VEC * sizeof(CT) == 32) {
+                ((uint4 *)(y + i))[0] = ((const uint4 *)r)[0];
+                ((uint4 *)(y + i))[1] = ((const uint4 *)r)[1];
+            } else {
+#pragma unroll
+                for (int k = 0; k < VEC; k++) y[i + k] = r[k];
+            }
+        } else {
+            for (int k = 0; k < VEC; k++)
+                if (i + k < n) y[i + k] = r[k];
+        }
+    }
+}
+
+// Streaming (re-reading) variants for rows too long for registers: one
+// 256-thread workgroup per row, LDS combine across its four waves.
+template <typename T>
+__device__ __forceinline__ T block_allreduce_sum(T v, T *lds)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, PT_WAVE);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[w] = v;
+    __syncthreads();
+    T r = 0;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) r = r + lds[i];
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ T block_allreduce_max(T v, T *lds)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmax_c(v, __shfl_xor(v, m, PT_WAVE));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[w] = v;
+    __syncthreads();
+    T r = lds[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = fmax_c(r, lds[i]);
+    return r;
+}
+
+template <int DT, typename OS>
+__global__ __launch_bounds__(256) void k_row_softmax_stream(const void *__restrict__ xin, int n,
+                                                            size_t ld, OS *__restrict__ out)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    __shared__ C lds[4];
+    const S *x = (const S *)xin + (size_t)blockIdx.x * ld;
+    OS *y = out + (size_t)blockIdx.x * (size_t)n;
+    C m = neg_inf<C>();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) m = fmax_c(m, RT<DT>::cv(x[i]));
+    m = block_allreduce_max(m, lds);
+    C s = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s = s + exp_c(RT<DT>::cv(x[i]) - m);
+    s = block_allreduce_sum(s, lds);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = (OS)(exp_c(RT<DT>::cv(x[i]) - m) / s);
+}
+
+template <int DT, typename CT>
+__global__ __launch_bounds__(256) void k_row_layernorm_stream(const void *__restrict__ xin, int n,
+                                                              CT eps, const CT *__restrict__ gamma,
+                                                              const CT *__restrict__ beta,
+                                                              CT *__restrict__ out)
+{
+    using S = typename RT<DT>::S;
+    __shared__ CT lds[4];
+    const S *x = (const S *)xin + (size_t)blockIdx.x * (size_t)n;
+    CT *y = out + (size_t)blockIdx.x * (size_t)n;
+    CT s = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) s = s + (CT)RT<DT>::cv(x[i]);
+    const CT mean = block_allreduce_sum(s, lds) / (CT)n;
+    CT q = 0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        CT d = (CT)RT<DT>::cv(x[i]) - mean;
+        q = q + d * d;
+    }
+    const CT dev = sqrt_c(block_allreduce_sum(q, lds) / (CT)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        CT t = ((CT)RT<DT>::cv(x[i]) - mean) / dev;
+        if (gamma) t = t * gamma[i];
+        if (beta) t = t + beta[i];
+        y[i] = t;
+    }
+}
+
+// ========================================================= generic paths
+// Generic element access for every dtype (integer sums wrap: the
+// accumulator is uint64 and is truncated on store, matching HostArray's
+// modular sums, contiguous_array_ce.c:1149-1161, 1229-1233).
+struct GenAcc {
+    int op, dt;
+    double d;      // float accumulation (sum/mean/prod/max/min of floats, mean of ints)
+    uint64_t u;    // integer sum/prod bits
+    int64_t si;    // signed integer extremum
+    uint64_t ui;   // unsigned integer extremum
+    int have;
+    Mom m;
+    double best; int bi;  // arg reductions (float compare in double; exact for <=32-bit ints)
+    int64_t bsi; uint64_t bui;
+};
+
+__device__ __forceinline__ bool is_signed_int(int dt) { return dt >= PT_INT8 && dt <= PT_INT64; }
+__device__ __forceinline__ bool is_unsigned_int(int dt)
+{
+    return (dt >= PT_UINT8 && dt <= PT_UINT64) || dt == PT_BOOL;
+}
+__device__ __forceinline__ bool is_float_dt(int dt)
+{
+    return dt == PT_FLOAT32 || dt == PT_FLOAT64 || dt == PT_FLOAT16 || dt == PT_BFLOAT16;
+}
+
+__device__ __forceinline__ int64_t load_i64(const void *p, int dt, size_t i)
+{
+    switch (dt) {
+    case PT_INT8: return ((const int8_t *)p)[i];
+    case PT_INT16: return ((const int16_t *)p)[i];
+    case PT_INT32: return ((const int32_t *)p)[i];
+    default: return ((const int64_t *)p)[i];
+    }
+}
+__device__ __forceinline__ uint64_t load_u64(const void *p, int dt, size_t i)
+{
+    switch (dt) {
+    case PT_UINT8: return ((const uint8_t *)p)[i];
+    case PT_BOOL: return ((const uint8_t *)p)[i] != 0;
+    case PT_UINT16: return ((const uint16_t *)p)[i];
+    case PT_UINT32: return ((const uint32_t *)p)[i];
+    default: return ((const uint64_t *)p)[i];
+    }
+}
+
+__device__ void gen_init(GenAcc &a, int op, int dt)
+{
+    a.op = op; a.dt = dt; a.have = 0; a.u = op == R_PROD ? 1 : 0;
+    a.d = op == R_PROD ? 1.0 : (op == R_MAX ? -INFINITY : (op == R_MIN ? INFINITY : 0.0));
+    a.si = 0; a.ui = 0; a.m = Mom{0, 0, 0};
+    a.best = op == R_ARGMAX ? -INFINITY : INFINITY; a.bi = 0;
+    a.bsi = op == R_ARGMAX ? INT64_MIN : INT64_MAX;
+    a.bui = op == R_ARGMAX ? 0 : UINT64_MAX;
+}
+
+__device__ void gen_add(GenAcc &a, const void *p, size_t off, int idx)
+{
+    const int dt = a.dt;
+    switch (a.op) {
+    case R_SUM:
+    case R_PROD:
+        if (is_float_dt(dt)) {
+            double v = load_as_double(p, dt, off);
+            if (dt == PT_FLOAT64) a.d = a.op == R_SUM ? a.d + v : a.d * v;
+            else a.d = a.op == R_SUM ? (double)((float)a.d + (float)v) : (double)((float)a.d * (float)v);
+        } else {
+            uint64_t v = is_signed_int(dt) ? (uint64_t)load_i64(p, dt, off) : load_u64(p, dt, off);
+            if (dt == PT_BOOL) a.u = a.op == R_SUM ? (a.u || v) : (a.u && v);
+            else a.u = a.op == R_SUM ? a.u + v : a.u * v;
+        }
+        break;
+    case R_MEAN: {
+        double v = is_float_dt(dt) ? load_as_double(p, dt, off)
+                 : is_signed_int(dt) ? (double)load_i64(p, dt, off) : (double)load_u64(p, dt, off);
+        if (dt == PT_FLOAT32 || dt == PT_FLOAT16 || dt == PT_BFLOAT16) a.d = (double)((float)a.d + (float)v);
+        else a.d = a.d + v;
+        break;
+    }
+    case R_MAX:
+    case R_MIN:
+        if (is_float_dt(dt)) {
+            double v = load_as_double(p, dt, off);
+            a.d = a.op == R_MAX ? fmax(a.d, v) : fmin(a.d, v);
+        } else if (is_signed_int(dt)) {
+            int64_t v = load_i64(p, dt, off);
+            if (!a.have || (a.op == R_MAX ? v > a.si : v < a.si)) a.si = v;
+            a.have = 1;
+        } else {
+            uint64_t v = load_u64(p, dt, off);
+            if (!a.have || (a.op == R_MAX ? v > a.ui : v < a.ui)) a.ui = v;
+            a.have = 1;
+        }
+        break;
+    case R_ARGMAX:
+    case R_ARGMIN: {
+        bool mx = a.op == R_ARGMAX;
+        if (is_float_dt(dt)) {
+            double v = load_as_double(p, dt, off);
+            if (mx ? v > a.best : v < a.best) { a.best = v; a.bi = idx; }
+        } else if (is_signed_int(dt)) {
+            int64_t v = load_i64(p, dt, off);
+            if (mx ? v > a.bsi : v < a.bsi) { a.bsi = v; a.bi = idx; }
+        } else {
+            uint64_t v = load_u64(p, dt, off);
+            if (mx ? v > a.bui : v < a.bui) { a.bui = v; a.bi = idx; }
+        }
+        break;
+    }
+    case R_VAR: {
+        double v = is_float_dt(dt) ? load_as_double(p, dt, off)
+                 : is_signed_int(dt) ? (double)load_i64(p, dt, off) : (double)load_u64(p, dt, off);
+        Mom s = {1.0, v, v - v};
+        a.m = mom_combine(a.m, s);
+        break;
+    }
+    }
+}
+
+__device__ void gen_merge(GenAcc &a, const GenAcc &b)
+{
+    const int dt = a.dt;
+    switch (a.op) {
+    case R_SUM:
+    case R_PROD:
+        if (is_float_dt(dt)) {
+            if (dt == PT_FLOAT64) a.d = a.op == R_SUM ? a.d + b.d : a.d * b.d;
+            else a.d = a.op == R_SUM ? (double)((float)a.d + (float)b.d) : (double)((float)a.d * (float)b.d);
+        } else if (dt == PT_BOOL) {
+            a.u = a.op == R_SUM ? (a.u || b.u) : (a.u && b.u);
+        } else {
+            a.u = a.op == R_SUM ? a.u + b.u : a.u * b.u;
+        }
+        break;
+    case R_MEAN:
+        if (dt == PT_FLOAT32 || dt == PT_FLOAT16 || dt == PT_BFLOAT16) a.d = (double)((float)a.d + (float)b.d);
+        else a.d = a.d + b.d;
+        break;
+    case R_MAX:
+    case R_MIN:
+        if (is_float_dt(dt)) {
+            a.d = a.op == R_MAX ? fmax(a.d, b.d) : fmin(a.d, b.d);
+        } else if (b.have) {
+            if (is_signed_int(dt)) {
+                if (!a.have || (a.op == R_MAX ? b.si > a.si : b.si < a.si)) a.si = b.si;
+            } else {
+                if (!a.have || (a.op == R_MAX ? b.ui > a.ui : b.ui < a.ui)) a.ui = b.ui;
+            }
+            a.have = 1;
+        }
+        break;
+    case R_ARGMAX:
+    case R_ARGMIN: {
+        bool mx = a.op == R_ARGMAX;
+        if (is_float_dt(dt)) {
+            if ((mx ? b.best > a.best : b.best < a.best) || (b.best == a.best && b.bi < a.bi)) {
+                a.best = b.best; a.bi = b.bi;
+            }
+        } else if (is_signed_int(dt)) {
+            if ((mx ? b.bsi > a.bsi : b.bsi < a.bsi) || (b.bsi == a.bsi && b.bi < a.bi)) {
+                a.bsi = b.bsi; a.bi = b.bi;
+            }
+        } else {
+            if ((mx ? b.bui > a.bui : b.bui < a.bui) || (b.bui == a.bui && b.bi < a.bi)) {
+                a.bui = b.bui; a.bi = b.bi;
+            }
+        }
+        break;
+    }
+    case R_VAR:
+        a.m = mom_combine(a.m, b.m);
+        break;
+    }
+}
+
+__device__ void store_bits_dt(void *out, int dt, size_t i, uint64_t bits)
+{
+    switch (dt) {
+    case PT_BOOL: ((uint8_t *)out)[i] = bits != 0; break;
+    case PT_INT8: case PT_UINT8: ((uint8_t *)out)[i] = (uint8_t)bits; break;
+    case PT_INT16: case PT_UINT16: ((uint16_t *)out)[i] = (uint16_t)bits; break;
+    case PT_INT32: case PT_UINT32: ((uint32_t *)out)[i] = (uint32_t)bits; break;
+    default: ((uint64_t *)out)[i] = bits; break;
+    }
+}
+
+struct GenParams {
+    int ndims;
+    int axis;          // -1: all elements
+    int shape[PT_MAX_DIMS];
+    size_t strides[PT_MAX_DIMS];
+    size_t count;      // reduced elements per output
+    size_t outputs;
+    size_t base;
+    int out_dt;
+    int correction;
+    int take_sqrt;
+};
+
+__device__ void gen_finish(const GenAcc &a, const GenParams &p, void *out, size_t o)
+{
+    const int dt = a.dt;
+    switch (a.op) {
+    case R_SUM:
+    case R_PROD:
+        if (is_float_dt(dt)) store_out(out, p.out_dt, o, a.d);
+        else store_bits_dt(out, p.out_dt, o, a.u);
+        break;
+    case R_MEAN: {
+        double r;
+        if (p.count == 0) r = NAN;
+        else if (p.out_dt == PT_FLOAT32) r = (double)((float)a.d / (float)p.count);
+        else r = a.d / (double)p.count;
+        store_out(out, p.out_dt, o, r);
+        break;
+    }
+    case R_MAX:
+    case R_MIN:
+        if (is_float_dt(dt)) store_out(out, p.out_dt, o, a.d);
+        else if (is_signed_int(dt)) store_bits_dt(out, p.out_dt, o, (uint64_t)a.si);
+        else store_bits_dt(out, p.out_dt, o, a.ui);
+        break;
+    case R_ARGMAX:
+    case R_ARGMIN:
+        ((int32_t *)out)[o] = a.bi;
+        break;
+    case R_VAR: {
+        double var = a.m.m2 / (double)(p.count - (size_t)p.correction);
+        store_out(out, p.out_dt, o, p.take_sqrt ? sqrt(var) : var);
+        break;
+    }
+    }
+}
+
+__device__ __forceinline__ size_t gen_offset(const GenParams &p, size_t o, size_t i)
+{
+    size_t off = p.base;
+    if (p.axis >= 0) {
+        size_t rem = o;
+        for (int d = p.ndims - 1; d >= 0; d--) {
+            if (d == p.axis) continue;
+            off += (rem % (size_t)p.shape[d]) * p.strides[d];
+            rem /= (size_t)p.shape[d];
+        }
+        off += i * p.strides[p.axis];
+    } else {
+        size_t rem = i;
+        for (int d = p.ndims - 1; d >= 0; d--) {
+            off += (rem % (size_t)p.shape[d]) * p.strides[d];
+            rem /= (size_t)p.shape[d];
+        }
+    }
+    return off;
+}
+
+// Block-cooperative merge of GenAcc through LDS (lane 0 holds the result).
+__device__ void gen_block_merge(GenAcc &a, GenAcc *lds)
+{
+    lds[threadIdx.x] = a;
+    __syncthreads();
+    for (unsigned s = blockDim.x / 2; s > 0; s >>= 1) {
+        if (threadIdx.x < s) gen_merge(lds[threadIdx.x], lds[threadIdx.x + s]);
+        __syncthreads();
+    }
+    a = lds[0];
+}
+
+// One workgroup per output, every layout.  Threads take contiguous slices
+// of the reduced index range so that sequential per-thread order (and
+// therefore the lowest-index tie rule) is preserved.
+__global__ __launch_bounds__(128) void k_strided_reduce(const void *__restrict__ x,
+                                                        void *__restrict__ out, int op, int dt,
+                                                        GenParams p)
+{
+    __shared__ GenAcc lds[128];
+    const size_t o = blockIdx.x;
+    if (o >= p.outputs) return;
+    GenAcc a;
+    gen_init(a, op, dt);
+    size_t per = (p.count + blockDim.x - 1) / blockDim.x;
+    size_t lo = threadIdx.x * per, hi = lo + per < p.count ? lo + per : p.count;
+    for (size_t i = lo; i < hi; i++) gen_add(a, x, gen_offset(p, o, i), (int)i);
+    gen_block_merge(a, lds);
+    if (threadIdx.x == 0) gen_finish(a, p, out, o);
+}
+
+// Contiguous (outer, n, inner) reduction over the middle axis: a 64x4
+// workgroup covers 64 consecutive inner positions (coalesced) and splits n
+// over its 4 waves in contiguous slices.
+__global__ __launch_bounds__(256) void k_column_reduce(const void *__restrict__ x,
+                                                       void *__restrict__ out, int op, int dt,
+                                                       size_t outer, size_t n, size_t inner,
+                                                       GenParams p)
+{
+    __shared__ GenAcc lds[4][64];
+    const int lx = threadIdx.x & 63, ly = threadIdx.x >> 6;
+    const size_t col = (size_t)blockIdx.x * 64 + lx;
+    const size_t o_outer = blockIdx.y;
+    GenAcc a;
+    gen_init(a, op, dt);
+    if (col < inner) {
+        size_t per = (n + 3) / 4;
+        size_t lo = ly * per, hi = lo + per < n ? lo + per : n;
+        const size_t base = o_outer * n * inner + col;
+        for (size_t i = lo; i < hi; i++) gen_add(a, x, base + i * inner, (int)i);
+    }
+    lds[ly][lx] = a;
+    __syncthreads();
+    if (ly == 0 && col < inner) {
+        for (int k = 1; k < 4; k++) gen_merge(a, lds[k][lx]);
+        gen_finish(a, p, out, o_outer * inner + col);
+    }
+}
+
+// Global reduction of a contiguous input: stage 1 writes one GenAcc per
+// workgroup (each takes a contiguous slice, so index ties resolve to the
+// lowest index), stage 2 merges them in order.
+__global__ __launch_bounds__(256) void k_global_partial(const void *__restrict__ x, int op, int dt,
+                                                        size_t count, size_t base,
+                                                        GenAcc *__restrict__ partials)
+{
+    __shared__ GenAcc lds[256];
+    size_t per_block = (count + gridDim.x - 1) / gridDim.x;
+    size_t blo = blockIdx.x * per_block;
+    size_t bhi = blo + per_block < count ? blo + per_block : count;
+    GenAcc a;
+    gen_init(a, op, dt);
+    if (blo < bhi) {
+        size_t len = bhi - blo;
+        size_t per = (len + blockDim.x - 1) / blockDim.x;
+        size_t lo = blo + threadIdx.x * per;
+        size_t hi = lo + per < bhi ? lo + per : bhi;
+        for (size_t i = lo; i < hi; i++) gen_add(a, x, base + i, (int)i);
+    }
+    gen_block_merge(a, lds);
+    if (threadIdx.x == 0) partials[blockIdx.x] = a;
+}
+
+__global__ __launch_bounds__(256) void k_global_final(const GenAcc *__restrict__ partials, int nparts,
+                                                      void *__restrict__ out, GenParams p)
+{
+    __shared__ GenAcc lds[256];
+    GenAcc a;
+    int per = (nparts + blockDim.x - 1) / blockDim.x;
+    int lo = threadIdx.x * per, hi = lo + per < nparts ? lo + per : nparts;
+    if (lo < hi) {
+        a = partials[lo];
+        for (int i = lo + 1; i < hi; i++) gen_merge(a, partials[i]);
+    } else {
+        gen_init(a, partials[0].op, partials[0].dt);
+    }
+    gen_block_merge(a, lds);
+    if (threadIdx.x == 0) gen_finish(a, p, out, 0);
+}
+
+// Fill used for empty-axis identities (sum 0, prod 1, mean NaN).
+__global__ void k_fill_identity(void *out, int out_dt, size_t n, double value)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    if (out_dt == PT_FLOAT32) ((float *)out)[i] = (float)value;
+    else if (out_dt == PT_FLOAT64) ((double *)out)[i] = value;
+    else store_bits_dt(out, out_dt, i, (uint64_t)(int64_t)value);
+}
+
+// ================================================================== host
+static int red_op_of(int op)
+{
+    switch (op) {
+    case PT_OP_REDUCE_SUM: return R_SUM;
+    case PT_OP_REDUCE_MEAN: return R_MEAN;
+    case PT_OP_REDUCE_MAX: return R_MAX;
+    case PT_OP_REDUCE_MIN: return R_MIN;
+    case PT_OP_REDUCE_PROD: return R_PROD;
+    case PT_OP_ARG_MAX: return R_ARGMAX;
+    case PT_OP_ARG_MIN: return R_ARGMIN;
+    default: return -1;
+    }
+}
+
+// Collapse the non-axis dims into rows with a uniform pitch; true if the
+// reduced axis is unit-stride and rows are equally spaced.
+static bool as_rows(const int *shape, const size_t *strides, int ndims, int axis,
+                    size_t *rows, size_t *ld)
+{
+    if (axis < 0 || (strides[axis] != 1 && shape[axis] != 1)) return false;
+    size_t r = 1, pitch = 0, expect = 0;
+    bool first = true;
+    for (int d = ndims - 1; d >= 0; d--) {
+        if (d == axis || shape[d] == 1) continue;
+        if (first) {
+            pitch = strides[d];
+            expect = strides[d] * (size_t)shape[d];
+            first = false;
+        } else {
+            if (strides[d] != expect) return false;
+            expect = strides[d] * (size_t)shape[d];
+        }
+        r *= (size_t)shape[d];
+    }
+    *rows = r;
+    // pitch may be below n (zero-stride broadcast rows): reads may overlap
+    *ld = first ? (size_t)shape[axis] : pitch;
+    return true;
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <int DT, int OP>
+static void launch_rows_t(const void *x, size_t rows, int n, size_t ld, void *out, int out_dt,
+                          int correction, int take_sqrt, hipStream_t s)
+{
+    constexpr int V = RT<DT>::V;
+    dim3 block(256), grid((unsigned)((rows + 3) / 4));
+    if (n % V == 0 && ld % V == 0 && aligned16(x))
+        k_row_reduce<DT, OP, V><<<grid, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+    else
+        k_row_reduce<DT, OP, 1><<<grid, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+}
+
+template <int DT>
+static bool launch_rows_dt(int rop, const void *x, size_t rows, int n, size_t ld, void *out,
+                           int out_dt, int correction, int take_sqrt, hipStream_t s)
+{
+    switch (rop) {
+    case R_SUM: launch_rows_t<DT, R_SUM>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_MEAN: launch_rows_t<DT, R_MEAN>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_MAX: launch_rows_t<DT, R_MAX>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_MIN: launch_rows_t<DT, R_MIN>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_PROD: launch_rows_t<DT, R_PROD>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_ARGMAX: launch_rows_t<DT, R_ARGMAX>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_ARGMIN: launch_rows_t<DT, R_ARGMIN>(x, rows, n, ld, out, out_dt, 0, 0, s); return true;
+    case R_VAR: launch_rows_t<DT, R_VAR>(x, rows, n, ld, out, out_dt, correction, take_sqrt, s); return true;
+    }
+    return false;
+}
+
+static bool launch_rows(int dt, int rop, const void *x, size_t rows, int n, size_t ld, void *out,
+                        int out_dt, int correction, int take_sqrt, hipStream_t s)
+{
+    switch (dt) {
+    case PT_FLOAT32: return launch_rows_dt<PT_FLOAT32>(rop, x, rows, n, ld, out, out_dt, correction, take_sqrt, s);
+    case PT_FLOAT64: return launch_rows_dt<PT_FLOAT64>(rop, x, rows, n, ld, out, out_dt, correction, take_sqrt, s);
+    case PT_BFLOAT16: return launch_rows_dt<PT_BFLOAT16>(rop, x, rows, n, ld, out, out_dt, correction, take_sqrt, s);
+    case PT_FLOAT16: return launch_rows_dt<PT_FLOAT16>(rop, x, rows, n, ld, out, out_dt, correction, take_sqrt, s);
+    default: return false;
+    }
+}
+
+static int result_dtype(int dtype, int rop)
+{
+    if (rop == R_ARGMAX || rop == R_ARGMIN) return PT_INT32;
+    if (rop == R_VAR) return (dtype == PT_FLOAT32 || dtype == PT_FLOAT16 || dtype == PT_BFLOAT16)
+                          ? PT_FLOAT32 : PT_FLOAT64;
+    if (rop == R_MEAN) return (dtype == PT_FLOAT32 || dtype == PT_FLOAT16 || dtype == PT_BFLOAT16)
+                           ? PT_FLOAT32 : PT_FLOAT64;
+    if (dtype == PT_FLOAT16 || dtype == PT_BFLOAT16) return PT_FLOAT32;
+    return dtype;
+}
+
+// Shared driver of pt_reduce / pt_arg_reduce / pt_moments.
+static pt_status reduce_driver(const void *input, void *output, int dtype, int rop, int out_dt,
+                               const int *shape, const size_t *strides, int ndims, int axis,
+                               size_t base_offset, int correction, int take_sqrt,
+                               pt_stream_t stream)
+{
+    PT_TRY(ensure_init());
+    if (!dtype_valid(dtype)) return fail(PT_ERR_INVALID, "reduction: unknown dtype %d", dtype);
+    if (ndims < 0 || ndims > PT_MAX_DIMS) return fail(PT_ERR_INVALID, "reduction: rank %d outside [0, 10]", ndims);
+    if (axis >= ndims) return fail(PT_ERR_INVALID, "reduction axis %d outside rank %d", axis, ndims);
+    for (int d = 0; d < ndims; d++)
+        if (shape[d] < 0) return fail(PT_ERR_INVALID, "reduction: negative extent");
+    hipStream_t s = stream_of(stream);
+    size_t total = numel(shape, ndims);
+    size_t count = axis < 0 ? total : (size_t)shape[axis];
+    size_t outputs = 1;
+    if (axis >= 0)
+        for (int d = 0; d < ndims; d++)
+            if (d != axis) outputs *= (size_t)shape[d];
+    if (outputs == 0) return PT_OK;
+    if (rop == R_VAR && (correction < 0 || (size_t)correction >= count))
+        return fail(PT_ERR_INVALID, "Variance correction must be non-negative and smaller than the reduced dimension");
+    if (count == 0) {
+        if (rop == R_MAX || rop == R_MIN)
+            return fail(PT_ERR_INVALID, "Min/max reduction has no identity for an empty axis");
+        if (rop == R_ARGMAX || rop == R_ARGMIN)
+            return fail(PT_ERR_INVALID, "Arg reduction has no identity for an empty axis");
+        double ident = rop == R_PROD ? 1.0 : (rop == R_MEAN ? NAN : 0.0);
+        k_fill_identity<<<(unsigned)((outputs + 255) / 256), 256, 0, s>>>(output, out_dt, outputs, ident);
+        PT_LAUNCH_CHECK("reduction identity fill");
+        return PT_OK;
+    }
+    if (count > (size_t)INT32_MAX && (rop == R_ARGMAX || rop == R_ARGMIN))
+        return fail(PT_ERR_INVALID, "arg reduction index exceeds int32");
+
+    GenParams p = {};
+    p.ndims = ndims;
+    p.axis = axis;
+    for (int d = 0; d < ndims; d++) {
+        p.shape[d] = shape[d];
+        p.strides[d] = strides[d];
+    }
+    p.count = count;
+    p.outputs = outputs;
+    p.base = base_offset;
+    p.out_dt = out_dt;
+    p.correction = correction;
+    p.take_sqrt = take_sqrt;
+
+    const size_t esz = dtype_size(dtype);
+    const char *xb = (const char *)input + base_offset * esz;
+
+    // rows: fast wave-per-row path (floating dtypes)
+    size_t rows = 0, ld = 0;
+    if (axis >= 0 && dtype_is_floating(dtype) && count <= (size_t)INT32_MAX &&
+        as_rows(shape, strides, ndims, axis, &rows, &ld)) {
+        if (launch_rows(dtype, rop, xb, rows, (int)count, ld, output, out_dt, correction, take_sqrt, s)) {
+            PT_LAUNCH_CHECK("row reduction");
+            counters().row_reduce_calls++;
+            return PT_OK;
+        }
+    }
+    bool contiguous = is_row_major(shape, strides, ndims);
+    if (axis < 0 && contiguous) {
+        int parts = (int)((total + 8191) / 8192);
+        if (parts > 1024) parts = 1024;
+        if (parts < 1) parts = 1;
+        GenAcc *partials = nullptr;
+        PT_TRY(scratch_alloc((void **)&partials, sizeof(GenAcc) * (size_t)parts, s));
+        k_global_partial<<<parts, 256, 0, s>>>(input, rop, dtype, total, base_offset, partials);
+        hipError_t e1 = hipGetLastError();
+        k_global_final<<<1, 256, 0, s>>>(partials, parts, output, p);
+        hipError_t e2 = hipGetLastError();
+        scratch_free(partials, s);
+        PT_TRY(check_hip(e1, "global reduction (partials)"));
+        PT_TRY(check_hip(e2, "global reduction (final)"));
+        counters().global_reduce_calls++;
+        return PT_OK;
+    }
+    if (axis >= 0 && contiguous && axis < ndims - 1) {
+        size_t outer = 1, inner = 1;
+        for (int d = 0; d < axis; d++) outer *= (size_t)shape[d];
+        for (int d = axis + 1; d < ndims; d++) inner *= (size_t)shape[d];
+        if (outer <= 65535) {
+            dim3 grid((unsigned)((inner + 63) / 64), (unsigned)outer);
+            k_column_reduce<<<grid, 256, 0, s>>>(xb, output, rop, dtype,
+                                                 outer, count, inner, p);
+            PT_LAUNCH_CHECK("column reduction");
+            counters().column_reduce_calls++;
+            return PT_OK;
+        }
+    }
+    if (outputs > 0x7fffffffu)
+        return fail(PT_ERR_INVALID, "reduction: too many outputs");
+    k_strided_reduce<<<(unsigned)outputs, 128, 0, s>>>(input, output, rop, dtype, p);
+    PT_LAUNCH_CHECK("strided reduction");
+    counters().strided_reduce_calls++;
+    return PT_OK;
+}
+
+// ---------------------------------------------------- fused row launchers
+template <int DT, typename OS>
+static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS *y, hipStream_t s)
+{
+    constexpr int V = RT<DT>::V;
+    dim3 block(256), grid((unsigned)((rows + 3) / 4));
+    bool vec = n % V == 0 && ld % V == 0 && aligned16(x) && aligned16(y);
+    int chunks = (n + 64 * V - 1) / (64 * V);
+    if (vec) {
+        switch (chunks) {
+        case 1: k_row_softmax<DT, V, 1, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 2: k_row_softmax<DT, V, 2, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 3: case 4: k_row_softmax<DT, V, 4, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 5: case 6: case 7: case 8:
+            k_row_softmax<DT, V, 8, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
+        default:
+            if (chunks <= 16 && sizeof(typename RT<DT>::C) == 4) {
+                k_row_softmax<DT, V, 16, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y);
+                return;
+            }
+            break;
+        }
+    }
+    k_row_softmax_stream<DT, OS><<<(unsigned)rows, 256, 0, s>>>(x, n, ld, y);
+}
+
+template <int DT, typename CT>
+static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, const CT *g,
+                                  const CT *b, CT *y, hipStream_t s)
+{
+    constexpr int V = RT<DT>::V;
+    dim3 block(256), grid((unsigned)((rows + 3) / 4));
+    bool vec = n % V == 0 && aligned16(x) && aligned16(y);
+    int chunks = (n + 64 * V - 1) / (64 * V);
+    if (vec) {
+        switch (chunks) {
+        case 1: k_row_layernorm<DT, V, 1, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 2: k_row_layernorm<DT, V, 2, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 3: case 4: k_row_layernorm<DT, V, 4, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 5: case 6: case 7: case 8:
+            k_row_layernorm<DT, V, 8, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        default:
+            if (chunks <= 16 && sizeof(CT) == 4) {
+                k_row_layernorm<DT, V, 16, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y);
+                return;
+            }
+            break;
+        }
+    }
+    k_row_layernorm_stream<DT, CT><<<(unsigned)rows, 256, 0, s>>>(x, n, eps, g, b, y);
+}
+
+// Strided -> contiguous permuted copy used to move the softmax axis last.
+__global__ void k_permute_copy(const void *__restrict__ x, void *__restrict__ y, int esz,
+                               GenParams p, size_t total)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    size_t rem = i, off = p.base;
+    for (int d = p.ndims - 1; d >= 0; d--) {
+        off += (rem % (size_t)p.shape[d]) * p.strides[d];
+        rem /= (size_t)p.shape[d];
+    }
+    switch (esz) {
+    case 1: ((uint8_t *)y)[i] = ((const uint8_t *)x)[off]; break;
+    case 2: ((uint16_t *)y)[i] = ((const uint16_t *)x)[off]; break;
+    case 4: ((uint32_t *)y)[i] = ((const uint32_t *)x)[off]; break;
+    default: ((uint64_t *)y)[i] = ((const uint64_t *)x)[off]; break;
+    }
+}
+
+static pt_status permute_copy(const void *x, void *y, int esz, const int *shape, const size_t *strides,
+                              int ndims, hipStream_t s)
+{
+    GenParams p = {};
+    p.ndims = ndims;
+    for (int d = 0; d < ndims; d++) {
+        p.shape[d] = shape[d];
+        p.strides[d] = strides[d];
+    }
+    size_t total = numel(shape, ndims);
+    if (!total) return PT_OK;
+    k_permute_copy<<<(unsigned)((total + 255) / 256), 256, 0, s>>>(x, y, esz, p, total);
+    PT_LAUNCH_CHECK("permute copy");
+    return PT_OK;
+}
+
+}  // namespace pt
+
+using namespace pt;
+
+extern "C" {
+
+int pt_reduce_result_dtype(int dtype, int op)
+{
+    int rop = red_op_of(op);
+    if (rop < 0 || !dtype_valid(dtype)) return -1;
+    return result_dtype(dtype, rop);
+}
+
+pt_status pt_reduce(const void *input, void *output, int dtype, int op,
+                    const int *shape, const size_t *strides, int ndims, int axis,
+                    size_t base_offset, pt_stream_t stream)
+{
+    int rop = red_op_of(op);
+    if (rop < 0 || rop == R_ARGMAX || rop == R_ARGMIN)
+        return fail(PT_ERR_INVALID, "pt_reduce: unsupported op %d", op);
+    return reduce_driver(input, output, dtype, rop, result_dtype(dtype, rop), shape, strides, ndims,
+                         axis, base_offset, 0, 0, stream);
+}
+
+pt_status pt_arg_reduce(const void *input, int32_t *output, int dtype, int op,
+                        const int *shape, const size_t *strides, int ndims, int axis,
+                        size_t base_offset, pt_stream_t stream)
+{
+    int rop = red_op_of(op);
+    if (rop != R_ARGMAX && rop != R_ARGMIN)
+        return fail(PT_ERR_INVALID, "pt_arg_reduce: op %d is not argmax/argmin", op);
+    return reduce_driver(input, output, dtype, rop, PT_INT32, shape, strides, ndims, axis,
+                         base_offset, 0, 0, stream);
+}
+
+pt_status pt_moments(const void *input, void *output, int input_dtype, int result_dtype_,
+                     const int *shape, const size_t *strides, int ndims, int axis,
+                     int correction, int standard_deviation, pt_stream_t stream)
+{
+    int expect = result_dtype(input_dtype, R_VAR);
+    if (result_dtype_ != expect)
+        return fail(PT_ERR_INVALID, "pt_moments: result dtype must be %s",
+                    expect == PT_FLOAT32 ? "float32" : "float64");
+    return reduce_driver(input, output, input_dtype, R_VAR, expect, shape, strides, ndims, axis, 0,
+                         correction, standard_deviation ? 1 : 0, stream);
+}
+
+pt_status pt_softmax(const void *input, void *output, int input_dtype, int output_dtype,
+                     const int *shape, const size_t *strides, int ndims, int axis,
+                     pt_stream_t stream)
+{
+    PT_TRY(ensure_init());
+    if (ndims < 1 || ndims > PT_MAX_DIMS || axis < 0 || axis >= ndims)
+        return fail(PT_ERR_INVALID, "Softmax axis is out of range for tensor rank %d", ndims);
+    int expect = (input_dtype == PT_FLOAT32 || input_dtype == PT_FLOAT16 || input_dtype == PT_BFLOAT16)
+                 ? PT_FLOAT32 : PT_FLOAT64;
+    if (output_dtype != expect)
+        return fail(PT_ERR_INVALID, "softmax output dtype must be %s", expect == PT_FLOAT32 ? "float32" : "float64");
+    if (!dtype_is_floating(input_dtype))
+        return fail(PT_ERR_UNSUPPORTED, "pt_softmax takes floating input; cast integers to float64 first");
+    hipStream_t s = stream_of(stream);
+    size_t total = numel(shape, ndims);
+    int n = shape[axis];
+    if (total == 0) {
+        if (n == 0) {
+            size_t others = 1;
+            for (int d = 0; d < ndims; d++) if (d != axis) others *= (size_t)shape[d];
+            if (others) return fail(PT_ERR_INVALID, "Min/max reduction has no identity for an empty axis");
+        }
+        return PT_OK;
+    }
+    // Move the axis last (contiguous) when the input is not already rows.
+    size_t rows = 0, ld = 0;
+    const void *src = input;
+    void *tmp_in = nullptr;
+    void *dst = output;
+    void *tmp_out = nullptr;
+    int perm_shape[PT_MAX_DIMS];
+    size_t perm_strides[PT_MAX_DIMS];
+    bool rowform = as_rows(shape, strides, ndims, axis, &rows, &ld) &&
+                   (axis == ndims - 1 || rows == 1);
+    // rows of the output must coincide with the contiguous output layout:
+    // only true when the axis is the last one (or the tensor is one row).
+    if (!rowform) {
+        int k = 0;
+        for (int d = 0; d < ndims; d++)
+            if (d != axis) { perm_shape[k] = shape[d]; perm_strides[k] = strides[d]; k++; }
+        perm_shape[k] = shape[axis];
+        perm_strides[k] = strides[axis];
+        size_t esz = dtype_size(input_dtype);
+        PT_TRY(scratch_alloc(&tmp_in, total * esz, s));
+        pt_status st = permute_copy(input, tmp_in, (int)esz, perm_shape, perm_strides, ndims, s);
+        if (st != PT_OK) { scratch_free(tmp_in, s); return st; }
+        src = tmp_in;
+        rows = total / (size_t)n;
+        ld = (size_t)n;
+        if (axis != ndims - 1) {
+            st = scratch_alloc(&tmp_out, total * dtype_size(output_dtype), s);
+            if (st != PT_OK) { scratch_free(tmp_in, s); return st; }
+            dst = tmp_out;
+        }
+    }
+    if (n > 0) {
+        switch (input_dtype) {
+        case PT_FLOAT32: launch_softmax_rows<PT_FLOAT32, float>(src, rows, n, ld, (float *)dst, s); break;
+        case PT_BFLOAT16: launch_softmax_rows<PT_BFLOAT16, float>(src, rows, n, ld, (float *)dst, s); break;
+        case PT_FLOAT16: launch_softmax_rows<PT_FLOAT16, float>(src, rows, n, ld, (float *)dst, s); break;
+        case PT_FLOAT64: launch_softmax_rows<PT_FLOAT64, double>(src, rows, n, ld, (double *)dst, s); break;
+        }
+    }
+    hipError_t err = hipGetLastError();
+    if (err == hipSuccess && tmp_out) {
+        // scatter rows back: output[..., axis, ...] from the permuted buffer
+        // the permuted buffer is contiguous over (others..., axis); build the
+        // strides that read it in the output's order
+        size_t pstr[PT_MAX_DIMS];
+        size_t pacc = (size_t)n;
+        pstr[axis] = 1;
+        for (int d = ndims - 1; d >= 0; d--) {
+            if (d == axis) continue;
+            pstr[d] = pacc;
+            pacc *= (size_t)shape[d];
+        }
+        pt_status st = permute_copy(tmp_out, output, (int)dtype_size(output_dtype), shape, pstr, ndims, s);
+        if (st != PT_OK) err = hipErrorLaunchFailure;
+    }
+    scratch_free(tmp_in, s);
+    scratch_free(tmp_out, s);
+    PT_TRY(check_hip(err, "softmax"));
+    counters().fused_row_calls++;
+    return PT_OK;
+}
+
+pt_status pt_layernorm(const void *input, void *output, int input_dtype, int compute_dtype,
+                       size_t rows, size_t n, double eps,
+                       const void *gamma, const void *beta, pt_stream_t stream)
+{
+    PT_TRY(ensure_init());
+    if (!(eps > 0.0) || !isfinite(eps))
+        return fail(PT_ERR_INVALID, "LayerNorm epsilon must be finite and greater than zero");
+    if (compute_dtype != PT_FLOAT32 && compute_dtype != PT_FLOAT64)
+        return fail(PT_ERR_INVALID, "LayerNorm compute dtype must be float32 or float64");
+    if (compute_dtype == PT_FLOAT32 && (!isfinite((float)eps) || (float)eps <= 0.0f))
+        return fail(PT_ERR_INVALID, "LayerNorm epsilon is not representable as float32");
+    if (n == 0 && rows) return fail(PT_ERR_INVALID, "LayerNorm cannot normalize an empty dimension");
+    if (n > (size_t)INT32_MAX) return fail(PT_ERR_INVALID, "LayerNorm row too long");
+    if (!rows) return PT_OK;
+    hipStream_t s = stream_of(stream);
+    int ni = (int)n;
+    if (compute_dtype == PT_FLOAT32) {
+        float e = (float)eps;
+        const float *g = (const float *)gamma, *b = (const float *)beta;
+        float *y = (float *)output;
+        switch (input_dtype) {
+        case PT_FLOAT32: launch_layernorm_rows<PT_FLOAT32, float>(input, rows, ni, e, g, b, y, s); break;
+        case PT_BFLOAT16: launch_layernorm_rows<PT_BFLOAT16, float>(input, rows, ni, e, g, b, y, s); break;
+        case PT_FLOAT16: launch_layernorm_rows<PT_FLOAT16, float>(input, rows, ni, e, g, b, y, s); break;
+        default: return fail(PT_ERR_INVALID, "float32 layerNorm takes f32/f16/bf16 input");
+        }
+    } else {
+        const double *g = (const double *)gamma, *b = (const double *)beta;
+        double *y = (double *)output;
+        switch (input_dtype) {
+        case PT_FLOAT64: launch_layernorm_rows<PT_FLOAT64, double>(input, rows, ni, eps, g, b, y, s); break;
+        case PT_FLOAT32: launch_layernorm_rows<PT_FLOAT32, double>(input, rows, ni, eps, g, b, y, s); break;
+        default: return fail(PT_ERR_INVALID, "float64 layerNorm takes f64/f32 input");
+        }
+    }
+    PT_LAUNCH_CHECK("layernorm");
+    counters().fused_row_calls++;
+    return PT_OK;
+}
+
+}  // extern "C"

@@ -30,8 +30,8 @@ OP = {
     "log": 8, "log1p": 9, "exp2": 10, "log2": 11, "log10": 12, "asin": 13,
     "acos": 14, "atan": 15, "sinh": 16, "cosh": 17, "tanh": 18, "sin": 19,
     "cos": 20, "tan": 21, "abs": 22, "neg": 23, "ceil": 26, "floor": 27,
-    "round": 28, "sum": 36, "mean": 37, "max": 38, "min": 39,
-    "argmax": 43, "argmin": 44,
+    "round": 28, "sum": 35, "mean": 36, "max": 37, "min": 38,
+    "argmax": 42, "argmin": 43,
 }
 
 _lib = None

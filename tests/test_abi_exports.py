@@ -1,0 +1,35 @@
+"""CPU-side checks of the C-ABI library: it loads without a GPU and exports
+every function declared in include/pt_hip.h (no compute calls)."""
+import ctypes
+import os
+import re
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER_DIR = os.path.join(ROOT, "include")
+
+
+def declared_functions(header):
+    text = open(header).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(pt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_device_library_exports_every_declared_symbol():
+    from phptensors import _abi
+    lib = ctypes.CDLL(_abi.DEVICE_LIB)
+    names = declared_functions(os.path.join(HEADER_DIR, "pt_hip.h"))
+    assert len(names) > 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes table covers the same set
+    assert sorted(_abi.SIGNATURES) == names
+
+
+def test_status_strings_without_device():
+    from phptensors import _abi
+    lib = _abi.load()
+    assert lib.pt_status_string(0) == b"success"
+    assert lib.pt_status_string(1) == b"invalid argument"
+    n = ctypes.c_int(-1)
+    assert lib.pt_device_count(ctypes.byref(n)) == 0
+    assert n.value >= 0
