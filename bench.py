@@ -1,0 +1,293 @@
+#!/usr/bin/env python3
+"""Benchmark of the php-gpu-tensors hot path on one MI355X.
+
+Metric: GEMM TFLOP/s + reduce/fused-eltwise HBM GB/s as a
+percentage of MI355X peak, 1 GPU.  Families measured:
+  reduce : config 2 — X[8192,4096] fp32 N(0,1): sum, mean, max, argmax, var
+           along the last axis, row softmax, layerNorm(eps=1e-5, gamma=1,
+           beta=0)
+  fused  : config 3 — Fusion plan tanh(x + y*z), x,z [16384,8192], y [8192],
+           replayed through hipGraph
+  gemm   : config 4 — batched A[32,2048,2048] @ B[32,2048,2048] in bf16
+           (fp32 accumulate), fp16 and fp32
+Inputs are resident in HBM before timing.  Kernels are captured into a HIP
+graph (so host launch overhead does not stretch the timed region) and timed
+with HIP events on the stream they run on.  Reduction inputs rotate over
+enough replicas to exceed the 256 MB Infinity Cache so that every launch
+streams from HBM.
+
+Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one
+GPU (the design note on sharding is in DESIGN.md).
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "php-gpu-tensors_amd"))
+
+import numpy as np  # noqa: E402
+
+from phptensors import _abi as A  # noqa: E402
+from phptensors import synthetic  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
+MALL_BYTES = 256 << 20
+
+
+class GraphTimer:
+    """Capture `launch()` `reps` times into a graph on a private stream and
+    time replays with HIP events recorded on that stream."""
+
+    def __init__(self, launch, reps):
+        lib = A.load()
+        self.lib = lib
+        self.stream = ctypes.c_void_p()
+        A.check(lib.pt_stream_create(ctypes.byref(self.stream)), "stream")
+        self.reps = reps
+        A.check(lib.pt_graph_begin_capture(self.stream), "capture")
+        try:
+            for r in range(reps):
+                launch(self.stream, r)
+        finally:
+            g = ctypes.c_void_p()
+            A.check(lib.pt_graph_end_capture(self.stream, ctypes.byref(g)), "end capture")
+        self.graph = g
+        self.ev0, self.ev1 = ctypes.c_void_p(), ctypes.c_void_p()
+        A.check(lib.pt_event_create(ctypes.byref(self.ev0)), "event")
+        A.check(lib.pt_event_create(ctypes.byref(self.ev1)), "event")
+
+    def run(self, replays):
+        lib = self.lib
+        A.check(lib.pt_event_record(self.ev0, self.stream), "record")
+        for _ in range(replays):
+            A.check(lib.pt_graph_launch(self.graph, self.stream), "graph launch")
+        A.check(lib.pt_event_record(self.ev1, self.stream), "record")
+        A.check(lib.pt_event_synchronize(self.ev1), "sync")
+        ms = ctypes.c_float()
+        A.check(lib.pt_event_elapsed_ms(self.ev0, self.ev1, ctypes.byref(ms)), "elapsed")
+        return ms.value / (replays * self.reps)  # ms per launch
+
+    def close(self):
+        self.lib.pt_graph_destroy(self.graph)
+        self.lib.pt_event_destroy(self.ev0)
+        self.lib.pt_event_destroy(self.ev1)
+        self.lib.pt_stream_destroy(self.stream)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- config 2
+def reduce_family(steps, warmup):
+    lib = A.load()
+    rows, n = 8192, 4096
+    x = synthetic.normal((rows, n), 0.0, 1.0, seed=2)
+    nbytes = x.nbytes
+    replicas = max(2, int(math.ceil(2 * MALL_BYTES / nbytes)))
+    xs = [A.to_device(x) for _ in range(replicas)]
+    shape, strides = A.ints([rows, n]), A.sizes([n, 1])
+    out = A.DeviceBuffer(rows * 4)
+    big = A.DeviceBuffer(rows * n * 4)
+    gamma = A.to_device(np.ones(n, np.float32))
+    beta = A.to_device(np.zeros(n, np.float32))
+    red_bytes = nbytes + rows * 4
+    row_bytes = 2 * nbytes
+
+    def mk(kind):
+        def launch(stream, r):
+            p = xs[r % replicas].ptr
+            if kind == "argmax":
+                st = lib.pt_arg_reduce(p, out.ptr, A.FLOAT32, A.OP["argmax"], shape, strides, 2, 1, 0, stream)
+            elif kind == "var":
+                st = lib.pt_moments(p, out.ptr, A.FLOAT32, A.FLOAT32, shape, strides, 2, 1, 0, 0, stream)
+            elif kind == "softmax":
+                st = lib.pt_softmax(p, big.ptr, A.FLOAT32, A.FLOAT32, shape, strides, 2, 1, stream)
+            elif kind == "layernorm":
+                st = lib.pt_layernorm(p, big.ptr, A.FLOAT32, A.FLOAT32, rows, n, 1e-5,
+                                      gamma.ptr, beta.ptr, stream)
+            else:
+                st = lib.pt_reduce(p, out.ptr, A.FLOAT32, A.OP[kind], shape, strides, 2, 1, 0, stream)
+            A.check(st, kind)
+        return launch
+
+    results = {}
+    for kind in ("sum", "mean", "max", "argmax", "var", "softmax", "layernorm"):
+        t = GraphTimer(mk(kind), reps=2 * replicas)
+        t.run(max(1, warmup))
+        ms = t.run(max(1, steps))
+        t.close()
+        b = row_bytes if kind in ("softmax", "layernorm") else red_bytes
+        gbs = b / (ms * 1e-3) / 1e9
+        results[kind] = {"ms": ms, "bytes": b, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS,
+                         "kernel": {"softmax": "k_row_softmax", "layernorm": "k_row_layernorm"}.get(
+                             kind, "k_row_reduce")}
+        log(f"reduce {kind}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM")
+    total_ms = sum(r["ms"] for r in results.values())
+    total_bytes = sum(r["bytes"] for r in results.values())
+    fam = {"workload": "config2: X[8192,4096] fp32 N(0,1) seed 2; sum/mean/max/argmax/var(-1), "
+                       "softmax(-1), layerNorm([1],1e-5,1,0)",
+           "ms_per_step": total_ms, "GB/s": total_bytes / (total_ms * 1e-3) / 1e9,
+           "frac": total_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "ops": results,
+           "replicas": replicas}
+    return fam
+
+
+# ---------------------------------------------------------------- config 4
+def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
+    lib = A.load()
+    bsz, m, n, k = 32, 2048, 2048, 2048
+    flops = 2.0 * bsz * m * n * k
+    a32 = synthetic.normal((bsz, m, k), 0.0, 0.02, seed=4)
+    b32 = synthetic.normal((bsz, k, n), 0.0, 0.02, seed=5)
+    results = {}
+    code = {"bf16": A.BFLOAT16, "fp16": A.FLOAT16, "fp32": A.FLOAT32}
+    for name in dtypes:
+        dt = code[name]
+        if dt == A.FLOAT32:
+            ha, hb = a32, b32
+        elif dt == A.FLOAT16:
+            ha, hb = a32.astype(np.float16).view(np.uint16), b32.astype(np.float16).view(np.uint16)
+        else:
+            ha, hb = _to_bf16(a32), _to_bf16(b32)
+        da, db = A.to_device(ha), A.to_device(hb)
+        dc = A.DeviceBuffer(bsz * m * n * ha.itemsize)
+        shp = A.ints([bsz, m, k])
+        st = A.sizes([m * k, k, 1])
+
+        def launch(stream, r, da=da, db=db, dc=dc, dt=dt):
+            A.check(lib.pt_matmul(da.ptr, db.ptr, dc.ptr, dt, shp, st, 3, shp, st, 3, shp, 3,
+                                  stream), "matmul")
+
+        t = GraphTimer(launch, reps=1)
+        t.run(max(1, warmup))
+        ms = t.run(max(1, steps))
+        t.close()
+        tf = flops / (ms * 1e-3) / 1e12
+        results[name] = {"ms": ms, "flop": flops, "TFLOP/s": tf, "peak": PEAK_TFLOPS[name],
+                         "frac": tf / PEAK_TFLOPS[name], "kernel": "k_gemm"}
+        log(f"gemm {name}: {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s  {100 * tf / PEAK_TFLOPS[name]:.1f}% of peak")
+        del da, db, dc
+    fam = {"workload": "config4: A,B [32,2048,2048] N(0,0.02) seeds 4/5; batched matmul "
+                       + "/".join(dtypes),
+           "ms_per_step": sum(r["ms"] for r in results.values()),
+           "frac": results[dtypes[0]]["frac"], "ops": results}
+    return fam
+
+
+def _to_bf16(x):
+    """float32 -> bfloat16 bits, round to nearest even (NaN-free input)."""
+    u = x.view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def reduce_cpu_baseline():
+    """The oracle (scalar C restatement, 1 thread) on the full config-2 input."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    rows, n = 8192, 4096
+    x = synthetic.normal((rows, n), 0.0, 1.0, seed=2)
+    ones, zeros = np.ones(n, np.float32), np.zeros(n, np.float32)
+    t0 = time.perf_counter()
+    O.reduce(x, O.F32, "sum", 1)
+    O.reduce(x, O.F32, "mean", 1)
+    O.reduce(x, O.F32, "max", 1)
+    O.arg_reduce(x, O.F32, "argmax", 1)
+    O.moments(x, O.F32, 1)
+    O.softmax_lastaxis(x)
+    O.layernorm_lastaxis(x, 1e-5, ones, zeros)
+    dt = time.perf_counter() - t0
+    total_bytes = 5 * (x.nbytes + rows * 4) + 2 * 2 * x.nbytes
+    return {"value": total_bytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": "full config-2 step (all 7 ops over X[8192,4096]) on one host core; "
+                      f"{dt:.2f} s", "seconds": dt}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--only", default="reduce,fused,gemm")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 128 MiB device copy first (reference for PMC byte counters)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py runs on one GPU only: this build has no multi-GPU path "
+              "(DESIGN.md describes how the hot path would shard).", file=sys.stderr)
+        sys.exit(2)
+    if os.environ.get("RANK", "0") != "0":
+        return
+    lib = A.load()
+    A.check(lib.pt_init(), "init")
+    info = A.device_info()
+    log(f"device {info.name.decode()} {info.arch.decode()} CUs={info.compute_units}")
+    if args.copy_calibration:
+        src = A.DeviceBuffer(128 << 20)
+        dst = A.DeviceBuffer(128 << 20)
+        for _ in range(3):
+            A.check(lib.pt_memcpy_d2d(dst.ptr, src.ptr, 128 << 20, None), "copy")
+        A.synchronize()
+        log("copy calibration: 3 x 128 MiB device-to-device copies")
+    fams = {}
+    t_wall = time.perf_counter()
+    only = set(args.only.split(","))
+    if "reduce" in only:
+        fams["reduce"] = reduce_family(args.steps, args.warmup)
+    if "gemm" in only:
+        fams["gemm"] = gemm_family(args.steps, args.warmup)
+    wall = time.perf_counter() - t_wall
+
+    # dominant kernel (largest time in a step) for the roofline object
+    dom = None
+    for fname, fam in fams.items():
+        for k, r in fam.get("ops", {}).items():
+            if dom is None or r["ms"] > dom[2]["ms"]:
+                dom = (fname, k, r)
+    roofline = None
+    if dom is not None:
+        r = dom[2]
+        if "GB/s" in r:
+            roofline = {"bound": "hbm", "kernel": r["kernel"], "op": f"{dom[0]}:{dom[1]}",
+                        "achieved": round(r["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(r["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None}
+        else:
+            roofline = {"bound": "mfma", "kernel": r["kernel"], "op": f"{dom[0]}:{dom[1]}",
+                        "achieved": round(r["TFLOP/s"], 1), "peak": r["peak"], "unit": "TFLOP/s",
+                        "frac": round(r["frac"], 4), "traffic": None}
+    fracs = [f["frac"] for f in fams.values()]
+    value = 100.0 * sum(fracs) / len(fracs) if fracs else 0.0
+    cpu = None
+    if not args.no_cpu and "reduce" in fams:
+        cpu = reduce_cpu_baseline()
+        cpu["cpu_model"] = platform.processor() or platform.machine()
+        cpu["nproc"] = os.cpu_count()
+    ms_step = sum(f["ms_per_step"] for f in fams.values())
+    line = {
+        "metric": "GEMM TFLOP/s + reduce/fused-eltwise HBM GB/s, % of MI355X peak, 1 GPU",
+        "value": round(value, 2),
+        "unit": "% of MI355X peak (mean over families)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic (SplitMix64/Box-Muller, fixed seeds)",
+        "config": {"workload": fams.get("reduce", {}).get("workload", ""),
+                   "families": sorted(fams)},
+        "families": {k: {kk: vv for kk, vv in v.items()} for k, v in fams.items()},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "wall_s": round(wall, 2),
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -230,6 +230,11 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
 pt_status pt_matmul_set_precision(int precision);
 const char *pt_matmul_precision_name(void);
 
+/* Tile override for the MFMA kernels, the tuning knob that replaces
+ * cuda_blas_tune_matmul (matmul_kernels.h:34-38): 0 = 256x128, 1 = 128x128,
+ * 2 = 64x64 workgroup tiles, -1 = automatic choice (default). */
+pt_status pt_matmul_set_tile(int tile);
+
 /* Backend counters (replace cuda_backend_info, backend_info.h:7-16). */
 typedef struct {
     char last_matmul[32];
@@ -249,21 +254,24 @@ pt_status pt_backend_info_reset(void);
 
 /* ----------------------------------------------------------- elementwise --
  * pt_broadcast replaces launch_broadcast (src/backends/cuda/broadcast_ops.h:
- * 10-16): out[i] = a[i] (op) b[i] over the output shape, operands already
- * aligned to the output rank with stride 0 on broadcast dims.  Arithmetic
- * ops (+ - * / ** maximum minimum) evaluate in out_dtype after converting
- * both operands; comparisons evaluate in compare_dtype and write bool.
+ * 10-16): out[i] = a[i] (op) b[i] over the output shape; strides_a/b are
+ * aligned to the output rank with stride 0 on broadcast dims.  Both
+ * operands are converted to the output dtype (float for f16/bf16 outputs)
+ * and the op is evaluated there, as broadcast_kernel_with_cast /
+ * _low_precision (broadcast_ops.cuh:62-150); comparisons write 1/0 in the
+ * output (promoted) dtype.  Ops: + - * / ** maximum minimum > < == != >= <=.
  * No contraction: a*b+c is two rounded operations. */
 pt_status pt_broadcast(const void *a, int dtype_a, const size_t *strides_a, size_t offset_a,
                        const void *b, int dtype_b, const size_t *strides_b, size_t offset_b,
-                       void *out, int dtype_out, int compare_dtype, int op,
+                       void *out, int dtype_out, int op,
                        const int *shape, int ndims, pt_stream_t stream);
 
 /* Replaces launch_scalar / launch_scalar_inv (scalar_ops.h:11-37):
- * out = in (op) scalar, or scalar (op) in when reverse != 0. */
+ * out = in (op) scalar, or scalar (op) in when reverse != 0, evaluated in
+ * the output dtype like pt_broadcast. */
 pt_status pt_scalar(const void *input, int dtype_in, const size_t *strides, size_t offset,
                     const pt_scalar_t *scalar, int reverse, void *out, int dtype_out,
-                    int compare_dtype, int op, const int *shape, int ndims, pt_stream_t stream);
+                    int op, const int *shape, int ndims, pt_stream_t stream);
 
 /* Replaces launch_unary_op (unary_ops.h:12-21): out = f(in), computed in
  * float32 for f32/f16/bf16 and float64 for f64; output dtype = input dtype. */

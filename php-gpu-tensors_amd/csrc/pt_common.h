@@ -31,7 +31,7 @@ pt_backend_info &counters();
 
 #define PT_LAUNCH_CHECK(what) PT_TRY(::pt::check_hip(hipGetLastError(), what))
 
-inline size_t dtype_size(int dtype)
+__host__ __device__ inline size_t dtype_size(int dtype)
 {
     switch (dtype) {
     case PT_FLOAT32: case PT_INT32: case PT_UINT32: return 4;

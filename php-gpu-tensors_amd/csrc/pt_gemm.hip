@@ -1,0 +1,575 @@
+// Batched GEMM for gfx950 on the MFMA matrix cores.
+//
+//   C[b] = A[b] @ B[b],  A: M x K, B: K x N, C: M x N row-major contiguous.
+//
+// bf16 / fp16: v_mfma_f32_32x32x16_{bf16,f16} (fp32 accumulate, RNE store
+// to the operand dtype, as __float2bfloat16_rn in the reference's
+// low_precision_matmul_nd_kernel, matmul_kernels.cu:738-791).
+// fp32: v_mfma_f32_32x32x2f32 (true fp32 products and accumulation; the
+// reference's strict-fp32 policy, matmul_kernels.cu:294-296).
+//
+// Tiling: a workgroup owns a BM x BN tile of C; its waves form a WM x WN
+// grid, each wave a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks held in
+// accumulator registers.  K advances in BK steps through two LDS stages
+// (global loads of step k+1 are in flight while step k runs on the matrix
+// cores).  Both operands are stored in LDS k-contiguous ([row][k], rows
+// padded by 16 bytes) so that every lane reads one 16-byte pack per MFMA
+// operand.  An operand whose k is not its contiguous dimension (row-major B,
+// or a transposed view of A) is transposed in registers between the global
+// load and the LDS store.
+//
+// Workgroup -> tile mapping is XCD-aware: dispatch places consecutive
+// workgroups on the 8 XCDs round-robin, so the linear id is remapped to give
+// each XCD a contiguous range of tiles, and tiles are walked in groups of
+// GROUP_M row-blocks so that co-resident workgroups share A and B panels in
+// their XCD's L2.
+#include "pt_common.h"
+
+#include <string.h>
+
+namespace pt {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+#define GEMM_MAX_BATCH_DIMS 8
+
+struct GemmArgs {
+    const void *a;
+    const void *b;
+    void *c;
+    int M, N, K;
+    long long a_sm, a_sk;  // A(m,k) = a[m * a_sm + k * a_sk]
+    long long b_sk, b_sn;  // B(k,n) = b[k * b_sk + n * b_sn]
+    int tiles_m, tiles_n;
+    int batch;
+    int nbd;               // batch dims
+    int bshape[GEMM_MAX_BATCH_DIMS];
+    long long bsa[GEMM_MAX_BATCH_DIMS];
+    long long bsb[GEMM_MAX_BATCH_DIMS];
+    int remap;             // total tiles divisible by 8: XCD remap on
+};
+
+// Element traits: storage type and elements per 16-byte pack.
+template <int DT> struct GE;
+template <> struct GE<PT_BFLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
+template <> struct GE<PT_FLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
+template <> struct GE<PT_FLOAT32> { using S = float; static constexpr int PK = 4; };
+
+template <int DT>
+__device__ __forceinline__ void store_c(void *c, size_t idx, float v)
+{
+    if constexpr (DT == PT_FLOAT32) ((float *)c)[idx] = v;
+    else if constexpr (DT == PT_BFLOAT16) ((uint16_t *)c)[idx] = float_to_bf16(v);
+    else ((uint16_t *)c)[idx] = float_to_f16(v);
+}
+
+// 16-byte pack type for register staging.
+typedef uint32_t Pack __attribute__((ext_vector_type(4)));
+
+// Gather PK k rows of VR consecutive r elements (raw[k][dword]) and emit VR
+// k-contiguous packs.
+template <int DT, int VR, int DW>
+__device__ __forceinline__ void transpose_to_packs(const uint32_t (&raw)[GE<DT>::PK][DW],
+                                                   Pack (&out)[VR])
+{
+    if constexpr (sizeof(typename GE<DT>::S) == 2) {
+        // 16-bit: dword d holds r = 2d (low half) and r = 2d+1 (high half)
+#pragma unroll
+        for (int r = 0; r < VR; r++) {
+            const int d = r >> 1;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                uint32_t lo = raw[2 * q][d], hi = raw[2 * q + 1][d];
+                out[r][q] = (r & 1) ? ((lo >> 16) | (hi & 0xffff0000u))
+                                      : ((lo & 0xffffu) | (hi << 16));
+            }
+        }
+    } else {
+        // fp32: raw[k][r] -> out[r].w[k]
+#pragma unroll
+        for (int r = 0; r < VR; r++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) out[r][q] = raw[q][r];
+    }
+}
+
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
+struct GemmCfg {
+    using S = typename GE<DT>::S;
+    static constexpr int PK = GE<DT>::PK;
+    static constexpr int T = 64 * WM * WN;
+    static constexpr int LDK = BK + PK;      // padded LDS row (elements)
+    static constexpr int WTM = BM / WM, WTN = BN / WN;
+    static constexpr int TM = WTM / 32, TN = WTN / 32;
+    // k-contiguous loads: 16-byte packs per thread
+    static constexpr int A_P = BM * BK / PK / T;
+    static constexpr int B_P = BN * BK / PK / T;
+    // r-contiguous loads: r elements per thread per k row
+    static constexpr int A_VR = BM * BK / (T * PK);
+    static constexpr int B_VR = BN * BK / (T * PK);
+    static_assert(BM % (32 * WM) == 0 && BN % (32 * WN) == 0, "wave tiling");
+    static_assert(BK % (2 * PK) == 0 || PK == 4, "k slices");
+    static_assert(A_P >= 1 && B_P >= 1, "load split");
+};
+
+// Load helpers ------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t to_bits(uint16_t v) { return v; }
+__device__ __forceinline__ uint32_t to_bits(float v) { return __float_as_uint(v); }
+
+template <typename S>
+__device__ __forceinline__ S load_elem_checked(const S *p, long long off, bool ok)
+{
+    return ok ? p[off] : (S)0;
+}
+
+// Stage one operand tile (R rows x BK k) from global memory into registers.
+// KC: k is the contiguous dimension of the source.
+template <int DT, int R, int BK, int T, bool KC, bool CHECK>
+struct TileLoader {
+    using S = typename GE<DT>::S;
+    static constexpr int PK = GE<DT>::PK;
+    static constexpr int P = R * BK / PK / T;         // packs per thread (KC)
+    static constexpr int VR = R * BK / (T * PK);      // r per thread (RC)
+    static constexpr int DW = (VR * (int)sizeof(S) + 3) / 4;  // dwords per RC row load
+    Pack kc[KC ? P : 1];
+    uint32_t rc[KC ? 1 : PK][KC ? 1 : (DW > 0 ? DW : 1)];
+
+    // src(r, k) = base[r * s_r + k * s_k]; rows [r0, r0+R) of r_total,
+    // k in [k0, k0+BK) of K.
+    __device__ __forceinline__ void load(const S *base, long long s_r, long long s_k, int r0,
+                                         int r_total, int k0, int K, int tid)
+    {
+        if constexpr (KC) {
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                int p = tid + j * T;
+                int r = p / (BK / PK), kp = p % (BK / PK);
+                int gr = r0 + r, gk = k0 + kp * PK;
+                if constexpr (!CHECK) {
+                    kc[j] = *(const Pack *)(base + (long long)gr * s_r + gk);
+                } else {
+                    Pack pk = {0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int e = 0; e < PK; e++) {
+                        S v = load_elem_checked(base, (long long)gr * s_r + (long long)(gk + e) * s_k,
+                                                gr < r_total && gk + e < K);
+                        pk[e * sizeof(S) / 4] |= to_bits(v) << (8 * ((e * sizeof(S)) % 4));
+                    }
+                    kc[j] = pk;
+                }
+            }
+        } else {
+            constexpr int RG = R / VR;  // r groups
+            int rg = tid % RG, kg = tid / RG;
+            int gr = r0 + rg * VR;
+#pragma unroll
+            for (int e = 0; e < PK; e++) {
+                int gk = k0 + kg * PK + e;
+                if constexpr (!CHECK) {
+                    const S *p = base + (long long)gk * s_k + gr;
+                    if constexpr (VR * sizeof(S) == 16) {
+                        uint4 v = *(const uint4 *)p;
+                        rc[e][0] = v.x; rc[e][1] = v.y; rc[e][2] = v.z; rc[e][3] = v.w;
+                    } else if constexpr (VR * sizeof(S) == 8) {
+                        uint2 v = *(const uint2 *)p;
+                        rc[e][0] = v.x; rc[e][1] = v.y;
+                    } else if constexpr (VR * sizeof(S) == 4) {
+                        rc[e][0] = *(const uint32_t *)p;
+                    } else {
+                        rc[e][0] = *(const uint16_t *)p;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < DW; q++) rc[e][q] = 0u;
+#pragma unroll
+                    for (int q = 0; q < VR; q++) {
+                        S v = load_elem_checked(base, (long long)gk * s_k + (long long)(gr + q) * s_r,
+                                                gk < K && gr + q < r_total);
+                        rc[e][q * sizeof(S) / 4] |= to_bits(v) << (8 * ((q * sizeof(S)) % 4));
+                    }
+                }
+            }
+        }
+    }
+
+    // Write the staged tile to LDS laid out [r][k] with row pitch LDK.
+    template <int LDK>
+    __device__ __forceinline__ void store(S *lds, int tid)
+    {
+        if constexpr (KC) {
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                int p = tid + j * T;
+                int r = p / (BK / PK), kp = p % (BK / PK);
+                *(Pack *)(lds + r * LDK + kp * PK) = kc[j];
+            }
+        } else {
+            constexpr int RG = R / VR;
+            int rg = tid % RG, kg = tid / RG;
+            Pack out[VR];
+            transpose_to_packs<DT, VR, DW>(rc, out);
+#pragma unroll
+            for (int q = 0; q < VR; q++)
+                *(Pack *)(lds + (rg * VR + q) * LDK + kg * PK) = out[q];
+        }
+    }
+};
+
+__device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long long &oa, long long &ob)
+{
+    oa = 0;
+    ob = 0;
+    for (int d = g.nbd - 1; d >= 0; d--) {
+        int c = b % g.bshape[d];
+        b /= g.bshape[d];
+        oa += (long long)c * g.bsa[d];
+        ob += (long long)c * g.bsb[d];
+    }
+}
+
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
+__global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs g)
+{
+    using C = GemmCfg<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK>;
+    using S = typename C::S;
+    constexpr int T = C::T, PK = C::PK, LDK = C::LDK, TM = C::TM, TN = C::TN;
+    constexpr int GROUP_M = 4;
+
+    __shared__ __attribute__((aligned(16))) S lds_a[2][BM * LDK];
+    __shared__ __attribute__((aligned(16))) S lds_b[2][BN * LDK];
+
+    // ---- tile selection (XCD-aware remap + grouped ordering)
+    const int ntile = g.tiles_m * g.tiles_n;
+    long long lin = blockIdx.x;
+    if (g.remap) {
+        long long total = (long long)ntile * g.batch;
+        long long per = total / 8;
+        lin = (lin % 8) * per + lin / 8;
+    }
+    const int bidx = (int)(lin / ntile);
+    const int t = (int)(lin % ntile);
+    const int group = t / (GROUP_M * g.tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gsz = min(g.tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (t % (GROUP_M * g.tiles_n)) % gsz;
+    const int tn = (t % (GROUP_M * g.tiles_n)) / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    long long oa, ob;
+    batch_offsets(g, bidx, oa, ob);
+    const S *A = (const S *)g.a + oa;
+    const S *B = (const S *)g.b + ob;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    TileLoader<DT, BM, BK, T, A_KC, CHECK> la;
+    TileLoader<DT, BN, BK, T, B_KC, CHECK> lb;
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    const int KT = (g.K + BK - 1) / BK;
+    // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
+    la.load(A, g.a_sm, g.a_sk, m0, g.M, 0, g.K, tid);
+    lb.load(B, g.b_sn, g.b_sk, n0, g.N, 0, g.K, tid);
+    la.template store<LDK>(lds_a[0], tid);
+    lb.template store<LDK>(lds_b[0], tid);
+    __syncthreads();
+
+    const int arow = wm * C::WTM + (lane & 31);
+    const int brow = wn * C::WTN + (lane & 31);
+    const int khalf = (lane >> 5) * PK;
+
+    for (int kt = 0; kt < KT; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) {
+            la.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 1) * BK, g.K, tid);
+            lb.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 1) * BK, g.K, tid);
+        }
+        const S *sa = lds_a[cur];
+        const S *sb = lds_b[cur];
+        if constexpr (DT == PT_FLOAT32) {
+#pragma unroll
+            for (int ks = 0; ks < BK; ks += 2 * PK) {
+                floatx4 fa[TM], fb[TN];
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+                    fa[i] = *(const floatx4 *)(sa + (arow + i * 32) * LDK + ks + khalf);
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    fb[j] = *(const floatx4 *)(sb + (brow + j * 32) * LDK + ks + khalf);
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e],
+                                                                              acc[i][j], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < BK; ks += 2 * PK) {
+                if constexpr (DT == PT_BFLOAT16) {
+                    bf16x8_t fa[TM], fb[TN];
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        fa[i] = *(const bf16x8_t *)(sa + (arow + i * 32) * LDK + ks + khalf);
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        fb[j] = *(const bf16x8_t *)(sb + (brow + j * 32) * LDK + ks + khalf);
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j],
+                                                                                 0, 0, 0);
+                } else {
+                    f16x8_t fa[TM], fb[TN];
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+                        fa[i] = *(const f16x8_t *)(sa + (arow + i * 32) * LDK + ks + khalf);
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+                        fb[j] = *(const f16x8_t *)(sb + (brow + j * 32) * LDK + ks + khalf);
+#pragma unroll
+                    for (int i = 0; i < TM; i++)
+#pragma unroll
+                        for (int j = 0; j < TN; j++)
+                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j],
+                                                                                0, 0, 0);
+                }
+            }
+        }
+        if (kt + 1 < KT) {
+            la.template store<LDK>(lds_a[cur ^ 1], tid);
+            lb.template store<LDK>(lds_b[cur ^ 1], tid);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: lane holds column n = lane%32 and rows
+    // 8*(e/4) + 4*(lane/32) + e%4 of each 32x32 block.
+    char *Cb = (char *)g.c + (size_t)bidx * (size_t)g.M * (size_t)g.N * sizeof(S);
+    const int col_l = lane & 31;
+    const int row_l = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * C::WTN + j * 32 + col_l;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
+                if (!CHECK || (m < g.M && n < g.N))
+                    store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
+            }
+        }
+}
+
+// ---------------------------------------------------------------- host side
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
+static void launch_cfg(const GemmArgs &g, hipStream_t s)
+{
+    long long grid = (long long)g.tiles_m * g.tiles_n * g.batch;
+    k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+}
+
+template <int DT, int BM, int BN, int BK, int WM, int WN>
+static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, hipStream_t s)
+{
+    if (check) {
+        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, true>(g, s);
+        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, true>(g, s);
+        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, true>(g, s);
+        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, true>(g, s);
+    } else {
+        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, false>(g, s);
+        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, false>(g, s);
+        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, false>(g, s);
+        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, false>(g, s);
+    }
+}
+
+// Tile configurations (BM, BN, BK, WM, WN).
+enum GemmTile { TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2 };
+
+static int g_tile_override = -1;
+
+// K step per LDS stage: 32 for 16-bit operands, 16 for fp32 (same bytes).
+template <int DT> struct GemmBK { static constexpr int v = DT == PT_FLOAT32 ? 16 : 32; };
+
+template <int DT>
+static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hipStream_t s)
+{
+    constexpr int BK = GemmBK<DT>::v;
+    switch (tile) {
+    case TILE_256x128:
+        g.tiles_m = (g.M + 255) / 256; g.tiles_n = (g.N + 127) / 128;
+        launch_layouts<DT, 256, 128, BK, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
+    case TILE_128x128:
+        g.tiles_m = (g.M + 127) / 128; g.tiles_n = (g.N + 127) / 128;
+        launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
+    default:
+        g.tiles_m = (g.M + 63) / 64; g.tiles_n = (g.N + 63) / 64;
+        launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
+    }
+}
+
+__global__ void k_zero_fill(uint8_t *p, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+static int g_precision = 0;
+
+}  // namespace pt
+
+using namespace pt;
+
+extern "C" {
+
+pt_status pt_matmul_set_precision(int precision)
+{
+    if (precision != 0 && precision != 1)
+        return fail(PT_ERR_INVALID, "Unknown matmul precision %d", precision);
+    g_precision = precision;
+    return PT_OK;
+}
+
+const char *pt_matmul_precision_name(void)
+{
+    // gfx950 has no reduced-precision fp32 (xf32) MFMA: both requests run
+    // true fp32 products, and the name says so.
+    return g_precision == 0 ? "fp32-strict" : "fp32-strict (tf32 unavailable on gfx950)";
+}
+
+// Tile override for sweeps: 0 = 256x128, 1 = 128x128, 2 = 64x64, -1 = auto.
+pt_status pt_matmul_set_tile(int tile)
+{
+    if (tile < -1 || tile > 2) return fail(PT_ERR_INVALID, "tile %d", tile);
+    g_tile_override = tile;
+    return PT_OK;
+}
+
+pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
+                    const int *shape_a, const size_t *strides_a, int nd_a,
+                    const int *shape_b, const size_t *strides_b, int nd_b,
+                    const int *shape_c, int nd_c, pt_stream_t stream)
+{
+    PT_TRY(ensure_init());
+    if (dtype != PT_FLOAT32 && dtype != PT_FLOAT16 && dtype != PT_BFLOAT16)
+        return fail(PT_ERR_INVALID, "matmul requires matching float32, float16 or bfloat16 operands");
+    if (nd_a < 2 || nd_b < 2 || nd_a > PT_MAX_DIMS || nd_b > PT_MAX_DIMS ||
+        shape_a[nd_a - 1] != shape_b[nd_b - 2])
+        return fail(PT_ERR_INVALID,
+                    "matmul requires rank >= 2, matching inner dimensions and broadcast-compatible batches");
+    // batch broadcast (tensor_matmul_shape, src/tensor_shape.h:46-59)
+    int bnd = (nd_a > nd_b ? nd_a : nd_b) - 2;
+    if (nd_c != bnd + 2) return fail(PT_ERR_INVALID, "matmul output rank mismatch");
+    if (bnd > GEMM_MAX_BATCH_DIMS) return fail(PT_ERR_INVALID, "matmul supports at most 8 batch dims");
+    GemmArgs g;
+    memset(&g, 0, sizeof(g));
+    g.M = shape_a[nd_a - 2];
+    g.K = shape_a[nd_a - 1];
+    g.N = shape_b[nd_b - 1];
+    if (shape_c[nd_c - 2] != g.M || shape_c[nd_c - 1] != g.N)
+        return fail(PT_ERR_INVALID, "matmul output shape mismatch");
+    long long batch = 1;
+    int k = 0;
+    for (int d = 0; d < bnd; d++) {
+        int ia = d - (bnd - (nd_a - 2)), ib = d - (bnd - (nd_b - 2));
+        int ea = ia >= 0 ? shape_a[ia] : 1, eb = ib >= 0 ? shape_b[ib] : 1;
+        if (ea != eb && ea != 1 && eb != 1)
+            return fail(PT_ERR_INVALID,
+                        "matmul requires rank >= 2, matching inner dimensions and broadcast-compatible batches");
+        int e = ea == 1 ? eb : ea;
+        if (e != shape_c[d]) return fail(PT_ERR_INVALID, "matmul output batch shape mismatch");
+        if (e == 1) continue;
+        g.bshape[k] = e;
+        g.bsa[k] = (ia >= 0 && ea != 1) ? (long long)strides_a[ia] : 0;
+        g.bsb[k] = (ib >= 0 && eb != 1) ? (long long)strides_b[ib] : 0;
+        batch *= e;
+        k++;
+    }
+    g.nbd = k;
+    hipStream_t s = stream_of(stream);
+    if (batch == 0 || g.M == 0 || g.N == 0) return PT_OK;
+    if (g.K == 0) {
+        // empty inner product: zeros (host_array_math.phpt:84-85)
+        size_t bytes = (size_t)batch * g.M * g.N * dtype_size(dtype);
+        k_zero_fill<<<(unsigned)((bytes + 255) / 256), 256, 0, s>>>((uint8_t *)c, bytes);
+        PT_LAUNCH_CHECK("matmul zero fill");
+        return PT_OK;
+    }
+    if (batch > 65535LL * 65535LL) return fail(PT_ERR_INVALID, "matmul batch too large");
+    g.a = a;
+    g.b = b;
+    g.c = c;
+    g.batch = (int)batch;
+    g.a_sm = (long long)strides_a[nd_a - 2];
+    g.a_sk = (long long)strides_a[nd_a - 1];
+    g.b_sk = (long long)strides_b[nd_b - 2];
+    g.b_sn = (long long)strides_b[nd_b - 1];
+
+    const int PKe = dtype == PT_FLOAT32 ? 4 : 8;
+    // layout classes: k-contiguous or row/col-contiguous; anything else is
+    // read element-wise by the checked kernel
+    bool a_kc = g.a_sk == 1 || g.K == 1;
+    bool a_rc = g.a_sm == 1 || g.M == 1;
+    bool b_kc = g.b_sk == 1 || g.K == 1;
+    bool b_rc = g.b_sn == 1 || g.N == 1;
+    if (!a_kc && !a_rc) a_kc = true;  // checked path handles arbitrary strides
+    if (!b_kc && !b_rc) b_kc = true;
+    int tile = g_tile_override;
+    if (tile < 0) {
+        long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 127) / 128) * batch;
+        tile = (g.M >= 256 && g.N >= 128 && t256 >= 256) ? TILE_256x128
+             : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
+    }
+    int bm = tile == TILE_256x128 ? 256 : tile == TILE_128x128 ? 128 : 64;
+    int bn = tile == TILE_64x64 ? 64 : 128;
+    const int BK = dtype == PT_FLOAT32 ? 16 : 32;
+    auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    bool vec_ok = aligned(a) && aligned(b);
+    // vector (unchecked) loads need whole tiles, 16-byte aligned rows and
+    // batch offsets that keep that alignment
+    bool check = !(g.M % bm == 0 && g.N % bn == 0 && g.K % BK == 0 && vec_ok);
+    if (!check) {
+        long long lda = a_kc ? g.a_sm : g.a_sk, ldb = b_kc ? g.b_sn : g.b_sk;
+        if ((a_kc ? g.a_sk : g.a_sm) != 1 || (b_kc ? g.b_sk : g.b_sn) != 1) check = true;
+        if (lda % PKe || ldb % PKe) check = true;
+        for (int d = 0; d < g.nbd; d++)
+            if (g.bsa[d] % PKe || g.bsb[d] % PKe) check = true;
+    }
+    long long total_tiles = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * batch;
+    g.remap = total_tiles % 8 == 0;
+    if (total_tiles > 0x7fffffffLL) return fail(PT_ERR_INVALID, "matmul grid too large");
+    switch (dtype) {
+    case PT_BFLOAT16: launch_dt<PT_BFLOAT16>(g, tile, a_kc, b_kc, check, s); break;
+    case PT_FLOAT16: launch_dt<PT_FLOAT16>(g, tile, a_kc, b_kc, check, s); break;
+    default: launch_dt<PT_FLOAT32>(g, tile, a_kc, b_kc, check, s); break;
+    }
+    PT_LAUNCH_CHECK("matmul");
+    counters().mfma_gemm_calls++;
+    snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s",
+             dtype == PT_FLOAT32 ? "mfma-fp32" : "mfma-low-precision");
+    return PT_OK;
+}
+
+}  // extern "C"

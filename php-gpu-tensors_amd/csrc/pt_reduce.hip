@@ -351,6 +351,19 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
     }
 }
 
+// 16-byte-aligned vector load of VEC values (VEC * sizeof(T) a multiple of 16).
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec16(const T *p, T (&v)[VEC])
+{
+    static_assert((VEC * sizeof(T)) % 16 == 0, "vector width");
+    constexpr int Q = VEC * sizeof(T) / 16;
+    union { uint4 raw[Q]; T t[VEC]; } u;
+#pragma unroll
+    for (int q = 0; q < Q; q++) u.raw[q] = ((const uint4 *)p)[q];
+#pragma unroll
+    for (int k = 0; k < VEC; k++) v[k] = u.t[k];
+}
+
 // Fused layerNorm over register-resident rows (cuda_array_ce.c:2295-2323):
 // mean, centered, biased variance of the centered values, eps inside the
 // sqrt, true division, then gamma and beta.
@@ -404,11 +417,22 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
     for (int c = 0; c < NCH; c++) {
         int i = (c * 64 + lane) * VEC;
         CT r[VEC];
+        CT g[VEC], b[VEC];
+        // gamma/beta follow x's chunk layout: vector loads, L2-resident
+        if (i + VEC <= n) {
+            if (gamma) load_vec16<CT, VEC>(gamma + i, g);
+            if (beta) load_vec16<CT, VEC>(beta + i, b);
+        } else {
+            for (int k = 0; k < VEC; k++) {
+                g[k] = gamma && i + k < n ? gamma[i + k] : (CT)1;
+                b[k] = beta && i + k < n ? beta[i + k] : (CT)0;
+            }
+        }
 #pragma unroll
         for (int k = 0; k < VEC; k++) {
             CT t = v[c][k] / dev;
-            if (gamma && i + k < n) t = t * gamma[i + k];
-            if (beta && i + k < n) t = t + beta[i + k];
+            if (gamma) t = t * g[k];
+            if (beta) t = t + b[k];
             r[k] = t;
         }
         if (i + VEC <= n) {
@@ -1095,7 +1119,8 @@ static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, con
 {
     constexpr int V = RT<DT>::V;
     dim3 block(256), grid((unsigned)((rows + 3) / 4));
-    bool vec = n % V == 0 && aligned16(x) && aligned16(y);
+    bool vec = n % V == 0 && aligned16(x) && aligned16(y) && (!g || aligned16(g)) &&
+               (!b || aligned16(b));
     int chunks = (n + 64 * V - 1) / (64 * V);
     if (vec) {
         switch (chunks) {

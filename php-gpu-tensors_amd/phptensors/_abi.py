@@ -112,15 +112,16 @@ SIGNATURES = {
                                  c_int_p, c_size_p, ctypes.c_int, c_int_p, ctypes.c_int, vp]),
     "pt_matmul_set_precision": (ctypes.c_int, [ctypes.c_int]),
     "pt_matmul_precision_name": (ctypes.c_char_p, []),
+    "pt_matmul_set_tile": (ctypes.c_int, [ctypes.c_int]),
     "pt_backend_info_get": (ctypes.c_int, [ctypes.POINTER(PtBackendInfo)]),
     "pt_backend_info_reset": (ctypes.c_int, []),
     "pt_broadcast": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, ctypes.c_size_t,
                                     vp, ctypes.c_int, c_size_p, ctypes.c_size_t,
-                                    vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    vp, ctypes.c_int, ctypes.c_int,
                                     c_int_p, ctypes.c_int, vp]),
     "pt_scalar": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, ctypes.c_size_t,
                                  ctypes.POINTER(PtScalar), ctypes.c_int, vp, ctypes.c_int,
-                                 ctypes.c_int, ctypes.c_int, c_int_p, ctypes.c_int, vp]),
+                                 ctypes.c_int, c_int_p, ctypes.c_int, vp]),
     "pt_unary": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, ctypes.c_size_t, vp, ctypes.c_int,
                                 c_int_p, ctypes.c_int, vp]),
     "pt_cast": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, ctypes.c_size_t, vp, ctypes.c_int,
@@ -247,6 +248,14 @@ class DeviceBuffer:
             check(load().pt_memcpy_d2h(out.ctypes.data, self.ptr, out.nbytes, self.stream),
                   "download")
         return out
+
+
+def matmul(a_buf, b_buf, c_buf, dtype, shape_a, strides_a, shape_b, strides_b, shape_c,
+           stream=None):
+    """pt_matmul on device buffers (pointers) with explicit views."""
+    check(load().pt_matmul(a_buf, b_buf, c_buf, dtype, ints(shape_a), sizes(strides_a),
+                           len(shape_a), ints(shape_b), sizes(strides_b), len(shape_b),
+                           ints(shape_c), len(shape_c), stream), "matmul")
 
 
 def to_device(array, stream=None):

@@ -1,0 +1,202 @@
+"""GPU parity: pt_matmul (MFMA kernels) against the CPU oracle (HostArray
+matmul restatement) on identical seeded bytes.
+
+Bars: integer-valued inputs give exact fp32 sums, so those outputs are
+bit-exact (also for bf16/fp16 outputs, which round the exact fp32 sum to
+nearest even).  Random fp32: |d| <= 1e-4 * sqrt(K) * (|A||B|)_ij.  Random
+bf16/fp16: |d| <= 1e-2 * max(|ref|, (|A||B|)_ij / sqrt(K)) against the
+oracle's fp32-accumulated, RNE-rounded product.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                     "reference_expectations.json")))
+DTS = {"float32": O.F32, "float16": O.F16, "bfloat16": O.BF16}
+
+
+@pytest.fixture(scope="module")
+def A():
+    from phptensors import _abi
+    _abi.check(_abi.load().pt_init(), "init")
+    yield _abi
+    _abi.load().pt_matmul_set_tile(-1)
+
+
+def run(A, a, b, dtype, shape_a=None, strides_a=None, shape_b=None, strides_b=None):
+    """a, b: contiguous storage arrays; optional view shape/strides (elements)."""
+    shape_a = tuple(a.shape if shape_a is None else shape_a)
+    shape_b = tuple(b.shape if shape_b is None else shape_b)
+    strides_a = [s // a.itemsize for s in a.strides] if strides_a is None else strides_a
+    strides_b = [s // b.itemsize for s in b.strides] if strides_b is None else strides_b
+    shape_c = O.matmul_shape(shape_a, shape_b)
+    da, db = A.to_device(a), A.to_device(b)
+    esz = 4 if dtype == O.F32 else 2
+    dc = A.DeviceBuffer(max(1, int(np.prod(shape_c)) * esz))
+    A.matmul(da.ptr, db.ptr, dc.ptr, dtype, shape_a, strides_a, shape_b, strides_b, shape_c)
+    return dc.download(O.NP_STORAGE[dtype], shape_c)
+
+
+def ref(a, b, dtype, **kw):
+    return O.matmul(a, b, dtype, **kw)
+
+
+@pytest.mark.parametrize("case", GOLDEN["matmul"], ids=lambda c: c["id"])
+def test_matmul_golden(A, case):
+    dt = DTS[case["dtype"]]
+    a = O.to_storage(np.array(case["a"], np.float64), dt).reshape(case["shape_a"])
+    b = O.to_storage(np.array(case["b"], np.float64), dt).reshape(case["shape_b"])
+    c = run(A, a, b, dt)
+    assert list(c.shape) == case["expected_shape"]
+    vals = O.from_storage(c, dt).astype(np.float64).ravel()
+    if "abs_tol" in case:
+        assert np.all(np.abs(vals - np.array(case["expected"])) < case["abs_tol"])
+    else:
+        assert vals.tolist() == [float(v) for v in case["expected"]]
+
+
+SHAPES = [(1, 64, 64, 64), (2, 256, 128, 64), (3, 100, 70, 33), (1, 512, 256, 512),
+          (4, 128, 384, 96), (1, 1, 300, 5), (2, 65, 1, 257), (1, 33, 17, 1)]
+
+
+def _ints(shape, seed, lo=-8, hi=8):
+    from phptensors import synthetic
+    return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
+
+
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2])
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bmnk", SHAPES, ids=str)
+def test_matmul_integer_exact(A, bmnk, dt, tile):
+    b_, m, n, k = bmnk
+    A.load().pt_matmul_set_tile(tile)
+    a32 = _ints((b_, m, k), seed=m * 7 + k)
+    b32 = _ints((b_, k, n), seed=n * 5 + k + 1)
+    a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+    got = run(A, a, b, dt)
+    assert np.array_equal(got, ref(a, b, dt))
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
+def test_matmul_transposed_views(A, dt, layout):
+    """A and/or B passed as transposed strided views (no copy)."""
+    m, n, k = 96, 160, 72
+    a32 = _ints((m, k), seed=1)
+    b32 = _ints((k, n), seed=2)
+    a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+    expect = ref(a, b, dt)
+    if layout[0] == "T":
+        at = np.ascontiguousarray(a.T)            # storage [k, m]
+        va = dict(shape_a=(m, k), strides_a=[1, m])
+        a_in = at
+    else:
+        a_in, va = a, {}
+    if layout[1] == "T":
+        bt = np.ascontiguousarray(b.T)            # storage [n, k]
+        vb = dict(shape_b=(k, n), strides_b=[1, k])
+        b_in = bt
+    else:
+        b_in, vb = b, {}
+    got = run(A, a_in, b_in, dt, **va, **vb)
+    assert np.array_equal(got, expect)
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16], ids=["f32", "bf16"])
+def test_matmul_batch_broadcast(A, dt):
+    # [1,64,64] @ [8,64,64] and [2,1,48,32] @ [1,3,32,40]
+    for sa, sb in (((1, 64, 64), (8, 64, 64)), ((2, 1, 48, 32), (1, 3, 32, 40)),
+                   ((64, 64), (5, 64, 64)), ((4, 64, 32), (32, 16))):
+        a = O.to_storage(_ints(sa, seed=3), dt)
+        b = O.to_storage(_ints(sb, seed=4), dt)
+        assert np.array_equal(run(A, a, b, dt), ref(a, b, dt))
+
+
+def test_matmul_accelerated_known_answers(A):
+    # ca_matmul_accelerated.phpt:9-29
+    row = np.ones((1, 100000), np.float32)
+    col = np.ones((100000, 1), np.float32)
+    assert run(A, row, col, O.F32)[0, 0] == 100000.0
+    ones = np.ones((64, 128), np.float32)
+    got = run(A, ones, ones, O.F32, shape_a=(128, 64), strides_a=[1, 128])
+    assert got.shape == (128, 128) and np.all(got == 64.0)
+    batch = np.ones((8, 64, 64), np.float32)
+    assert np.all(run(A, batch, batch, O.F32) == 64.0)
+    multi = np.ones((2, 4, 64, 64), np.float32)
+    assert np.all(run(A, multi, multi, O.F32) == 64.0)
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
+def test_matmul_random_within_tolerance(A, dt):
+    from phptensors import synthetic
+    b_, m, n, k = 2, 256, 384, 1024
+    a32 = synthetic.normal((b_, m, k), 0.0, 1.0, seed=41)
+    b32 = synthetic.normal((b_, k, n), 0.0, 1.0, seed=42)
+    a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+    got = O.from_storage(run(A, a, b, dt), dt).astype(np.float64)
+    r = O.from_storage(ref(a, b, dt), dt).astype(np.float64)
+    af = O.from_storage(a, dt).astype(np.float64)
+    bf = O.from_storage(b, dt).astype(np.float64)
+    scale = np.abs(af) @ np.abs(bf)
+    if dt == O.F32:
+        tol = 1e-4 * math.sqrt(k) * scale
+    else:
+        tol = 1e-2 * np.maximum(np.abs(r), scale / math.sqrt(k))
+    assert np.all(np.abs(got - r) <= tol)
+
+
+def test_matmul_errors(A):
+    from phptensors._abi import InvalidArgumentException
+    a = np.ones((2, 3), np.float32)
+    with pytest.raises(InvalidArgumentException):
+        run(A, a, a, O.F32)  # inner mismatch via shape check
+    x = np.ones((3,), np.float32)
+    with pytest.raises(InvalidArgumentException):
+        A.matmul(A.to_device(x).ptr, A.to_device(x).ptr, A.DeviceBuffer(4).ptr, O.F32,
+                 (3,), [1], (3,), [1], (1,))
+    with pytest.raises(InvalidArgumentException):
+        A.matmul(A.to_device(a).ptr, A.to_device(a).ptr, A.DeviceBuffer(64).ptr, O.F64,
+                 (2, 3), [3, 1], (3, 2), [2, 1], (2, 2))
+
+
+def test_matmul_empty(A):
+    a = np.zeros((2, 0), np.float32)
+    b = np.zeros((0, 3), np.float32)
+    assert np.array_equal(run(A, a, b, O.F32), np.zeros((2, 3), np.float32))
+    assert run(A, np.zeros((0, 2, 3), np.float32), np.ones((3, 2), np.float32), O.F32).shape == (0, 2, 2)
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32], ids=["bf16", "f16", "f32"])
+def test_config4_full_size_sampled(A, dt):
+    """A,B [32,2048,2048] N(0,0.02): 512 sampled outputs against float64 dot
+    products (tolerances above), plus exact RNE of the sampled fp32 sums."""
+    from phptensors import synthetic
+    shape = (32, 2048, 2048)
+    a32 = synthetic.normal(shape, 0.0, 0.02, seed=4)
+    b32 = synthetic.normal(shape, 0.0, 0.02, seed=5)
+    a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+    del a32, b32
+    got = run(A, a, b, dt)
+    af = O.from_storage(a, dt)
+    bf = O.from_storage(b, dt)
+    rng = np.random.default_rng(6)
+    idx = rng.integers(0, [32, 2048, 2048], size=(512, 3))
+    k = 2048
+    for bb, i, j in idx:
+        row = af[bb, i, :].astype(np.float64)
+        col = bf[bb, :, j].astype(np.float64)
+        exact = float(row @ col)
+        scale = float(np.abs(row) @ np.abs(col))
+        g = float(O.from_storage(np.array([got[bb, i, j]]), dt)[0])
+        if dt == O.F32:
+            assert abs(g - exact) <= 1e-4 * math.sqrt(k) * scale
+        else:
+            assert abs(g - exact) <= 1e-2 * max(abs(exact), scale / math.sqrt(k))
