@@ -219,6 +219,38 @@ struct TileLoader {
     }
 };
 
+template <int DT> struct FragT;
+template <> struct FragT<PT_BFLOAT16> { using type = bf16x8_t; };
+template <> struct FragT<PT_FLOAT16> { using type = f16x8_t; };
+template <> struct FragT<PT_FLOAT32> { using type = floatx4; };
+
+// acc[i][j] += A-fragment i x B-fragment j for one k-slice.
+template <int DT, int TM, int TN>
+__device__ __forceinline__ void mfma_block(floatx16 (&acc)[TM][TN],
+                                           const typename FragT<DT>::type (&fa)[TM],
+                                           const typename FragT<DT>::type (&fb)[TN])
+{
+    if constexpr (DT == PT_FLOAT32) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (DT == PT_BFLOAT16)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+    }
+}
+
 __device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long long &oa, long long &ob)
 {
     oa = 0;
@@ -231,8 +263,9 @@ __device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long lon
     }
 }
 
-template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
-__global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs g)
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK,
+          int SCHED = 0, int MINW = 1>
+__global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 {
     using C = GemmCfg<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK>;
     using S = typename C::S;
@@ -268,8 +301,11 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs g)
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
-    TileLoader<DT, BM, BK, T, A_KC, CHECK> la;
-    TileLoader<DT, BN, BK, T, B_KC, CHECK> lb;
+    // Two register staging sets: the global loads of tile k+2 are issued
+    // while tile k runs on the matrix cores and tile k+1 waits in the other
+    // set, giving the loads two K steps of MFMA work to arrive.
+    TileLoader<DT, BM, BK, T, A_KC, CHECK> la[2];
+    TileLoader<DT, BN, BK, T, B_KC, CHECK> lb[2];
 
     floatx16 acc[TM][TN];
 #pragma unroll
@@ -281,82 +317,77 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs g)
 
     const int KT = (g.K + BK - 1) / BK;
     // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
-    la.load(A, g.a_sm, g.a_sk, m0, g.M, 0, g.K, tid);
-    lb.load(B, g.b_sn, g.b_sk, n0, g.N, 0, g.K, tid);
-    la.template store<LDK>(lds_a[0], tid);
-    lb.template store<LDK>(lds_b[0], tid);
+    la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, g.K, tid);
+    lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, g.K, tid);
+    if (KT > 1) {
+        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, g.K, tid);
+        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, g.K, tid);
+    }
+    la[0].template store<LDK>(lds_a[0], tid);
+    lb[0].template store<LDK>(lds_b[0], tid);
     __syncthreads();
 
     const int arow = wm * C::WTM + (lane & 31);
     const int brow = wn * C::WTN + (lane & 31);
     const int khalf = (lane >> 5) * PK;
+    // One k-slice feeds one MFMA per (i, j) block: 16 k for 16-bit operands,
+    // 8 k (four 32x32x2 MFMAs) for fp32.  Fragments of slice s+1 are read
+    // from LDS into the second register set while slice s runs on the
+    // matrix cores, so LDS latency overlaps MFMA execution.
+    constexpr int KS = 2 * PK;
+    constexpr int NS = BK / KS;
+    using Frag = typename FragT<DT>::type;
+    Frag fa[2][TM], fb[2][TN];
+    auto read_frags = [&](const S *sa, const S *sb, int slice, Frag (&ra)[TM], Frag (&rb)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+            ra[i] = *(const Frag *)(sa + (arow + i * 32) * LDK + slice * KS + khalf);
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            rb[j] = *(const Frag *)(sb + (brow + j * 32) * LDK + slice * KS + khalf);
+    };
+    read_frags(lds_a[0], lds_b[0], 0, fa[0], fb[0]);
 
-    for (int kt = 0; kt < KT; kt++) {
+    // step kt: W holds tile kt+1 (to LDS after the MFMAs), L receives tile kt+2
+    auto step = [&](int kt, TileLoader<DT, BM, BK, T, A_KC, CHECK> &wa,
+                    TileLoader<DT, BN, BK, T, B_KC, CHECK> &wb,
+                    TileLoader<DT, BM, BK, T, A_KC, CHECK> &la_,
+                    TileLoader<DT, BN, BK, T, B_KC, CHECK> &lb_) {
         const int cur = kt & 1;
-        if (kt + 1 < KT) {
-            la.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 1) * BK, g.K, tid);
-            lb.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 1) * BK, g.K, tid);
+        if (kt + 2 < KT) {
+            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, g.K, tid);
+            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, g.K, tid);
         }
-        const S *sa = lds_a[cur];
-        const S *sb = lds_b[cur];
-        if constexpr (DT == PT_FLOAT32) {
 #pragma unroll
-            for (int ks = 0; ks < BK; ks += 2 * PK) {
-                floatx4 fa[TM], fb[TN];
+        for (int sl = 0; sl < NS; sl++) {
+            if (sl + 1 < NS)
+                read_frags(lds_a[cur], lds_b[cur], sl + 1, fa[(sl + 1) & 1], fb[(sl + 1) & 1]);
+            mfma_block<DT, TM, TN>(acc, fa[sl & 1], fb[sl & 1]);
+            if constexpr (SCHED == 1) {
+                __builtin_amdgcn_iglp_opt(0);
+            } else if constexpr (SCHED == 2) {
+                __builtin_amdgcn_iglp_opt(1);
+            } else if constexpr (SCHED == 3) {
+                // interleave: one MFMA, then one LDS read, for the reads of
+                // the next slice; remaining MFMAs follow
 #pragma unroll
-                for (int i = 0; i < TM; i++)
-                    fa[i] = *(const floatx4 *)(sa + (arow + i * 32) * LDK + ks + khalf);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    fb[j] = *(const floatx4 *)(sb + (brow + j * 32) * LDK + ks + khalf);
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-#pragma unroll
-                        for (int j = 0; j < TN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e],
-                                                                              acc[i][j], 0, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < BK; ks += 2 * PK) {
-                if constexpr (DT == PT_BFLOAT16) {
-                    bf16x8_t fa[TM], fb[TN];
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-                        fa[i] = *(const bf16x8_t *)(sa + (arow + i * 32) * LDK + ks + khalf);
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        fb[j] = *(const bf16x8_t *)(sb + (brow + j * 32) * LDK + ks + khalf);
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-#pragma unroll
-                        for (int j = 0; j < TN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j],
-                                                                                 0, 0, 0);
-                } else {
-                    f16x8_t fa[TM], fb[TN];
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-                        fa[i] = *(const f16x8_t *)(sa + (arow + i * 32) * LDK + ks + khalf);
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        fb[j] = *(const f16x8_t *)(sb + (brow + j * 32) * LDK + ks + khalf);
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-#pragma unroll
-                        for (int j = 0; j < TN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j],
-                                                                                0, 0, 0);
+                for (int q = 0; q < TM + TN; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
                 }
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
             }
         }
         if (kt + 1 < KT) {
-            la.template store<LDK>(lds_a[cur ^ 1], tid);
-            lb.template store<LDK>(lds_b[cur ^ 1], tid);
+            wa.template store<LDK>(lds_a[cur ^ 1], tid);
+            wb.template store<LDK>(lds_b[cur ^ 1], tid);
         }
         __syncthreads();
+        if (kt + 1 < KT) read_frags(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, fa[0], fb[0]);
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, la[1], lb[1], la[0], lb[0]);
+        if (kt + 1 < KT) step(kt + 1, la[0], lb[0], la[1], lb[1]);
     }
 
     // ---- epilogue: lane holds column n = lane%32 and rows
@@ -379,10 +410,37 @@ __global__ __launch_bounds__(64 * WM * WN) void k_gemm(GemmArgs g)
 }
 
 // ---------------------------------------------------------------- host side
+static int g_sched = 2;
+
 template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
 static void launch_cfg(const GemmArgs &g, hipStream_t s)
 {
     long long grid = (long long)g.tiles_m * g.tiles_n * g.batch;
+    if constexpr (BM == 256 && BN == 128 && A_KC && !B_KC && !CHECK && DT != PT_FLOAT32) {
+        // two workgroups per CU: waves sharing a SIMD belong to different
+        // workgroups, so their barrier phases do not coincide
+        if (g_sched >= 4) {
+            if (g_sched == 4)
+                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 0, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            else
+                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            return;
+        }
+    }
+    if constexpr (BM == 256 && BN == 256 && A_KC && !B_KC && !CHECK && DT != PT_FLOAT32) {
+        if (g_sched == 1) {
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 1><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            return;
+        }
+        if (g_sched == 2) {
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            return;
+        }
+        if (g_sched == 3) {
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 3><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            return;
+        }
+    }
     k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
 }
 
@@ -402,8 +460,17 @@ static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, 
     }
 }
 
-// Tile configurations (BM, BN, BK, WM, WN).
-enum GemmTile { TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2 };
+// Tile configurations: workgroup tile BM x BN, K step (1x or 2x the base
+// BK of the dtype), wave grid WM x WN.
+enum GemmTile {
+    TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
+    TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
+    TILE_COUNT = 8
+};
+struct TileInfo { int bm, bn, kmul; };
+static const TileInfo kTiles[TILE_COUNT] = {
+    {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
+    {256, 256, 1}, {256, 256, 2}};
 
 static int g_tile_override = -1;
 
@@ -414,19 +481,23 @@ template <int DT>
 static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hipStream_t s)
 {
     constexpr int BK = GemmBK<DT>::v;
+    const TileInfo &ti = kTiles[tile];
+    g.tiles_m = (g.M + ti.bm - 1) / ti.bm;
+    g.tiles_n = (g.N + ti.bn - 1) / ti.bn;
     switch (tile) {
     case TILE_256x128:
-        g.tiles_m = (g.M + 255) / 256; g.tiles_n = (g.N + 127) / 128;
-        launch_layouts<DT, 256, 128, BK, 2, 2>(g, a_kc, b_kc, check, s);
-        break;
-    case TILE_128x128:
-        g.tiles_m = (g.M + 127) / 128; g.tiles_n = (g.N + 127) / 128;
+        if constexpr (DT != PT_FLOAT32) {
+            if (!check && a_kc && !b_kc) {
+                launch_cfg<DT, 256, 128, BK, 2, 2, true, false, false>(g, s);
+                break;
+            }
+        }
         launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s);
         break;
-    default:
-        g.tiles_m = (g.M + 63) / 64; g.tiles_n = (g.N + 63) / 64;
-        launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s);
-        break;
+    case TILE_128x128: launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
+    case TILE_256x256: launch_layouts<DT, 256, 256, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
+    case TILE_256x256_K2: launch_layouts<DT, 256, 256, 2 * BK, 2, 4>(g, a_kc, b_kc, check, s); break;
+    default: launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     }
 }
 
@@ -459,10 +530,21 @@ const char *pt_matmul_precision_name(void)
     return g_precision == 0 ? "fp32-strict" : "fp32-strict (tf32 unavailable on gfx950)";
 }
 
-// Tile override for sweeps: 0 = 256x128, 1 = 128x128, 2 = 64x64, -1 = auto.
+// Instruction-scheduling variant of the 256x256 kernels (tuning knob):
+// 0 = compiler default, 1/2 = iglp strategies, 3 = MFMA/LDS interleave.
+pt_status pt_matmul_set_schedule(int sched)
+{
+    if (sched < 0 || sched > 5) return fail(PT_ERR_INVALID, "schedule %d", sched);
+    g_sched = sched;
+    return PT_OK;
+}
+
+// Tile override (see kTiles), -1 = automatic.
 pt_status pt_matmul_set_tile(int tile)
 {
-    if (tile < -1 || tile > 2) return fail(PT_ERR_INVALID, "tile %d", tile);
+    if (tile < -1 || tile >= TILE_COUNT || tile == TILE_256x128_K2 ||
+        tile == TILE_256x256_W4 || tile == TILE_256x256_W4_K2)
+        return fail(PT_ERR_INVALID, "tile %d is not built", tile);
     g_tile_override = tile;
     return PT_OK;
 }
@@ -538,13 +620,12 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     if (!b_kc && !b_rc) b_kc = true;
     int tile = g_tile_override;
     if (tile < 0) {
-        long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 127) / 128) * batch;
-        tile = (g.M >= 256 && g.N >= 128 && t256 >= 256) ? TILE_256x128
+        long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
+        tile = (g.M >= 256 && g.N >= 256 && t256 >= 256) ? TILE_256x256
              : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
     }
-    int bm = tile == TILE_256x128 ? 256 : tile == TILE_128x128 ? 128 : 64;
-    int bn = tile == TILE_64x64 ? 64 : 128;
-    const int BK = dtype == PT_FLOAT32 ? 16 : 32;
+    int bm = kTiles[tile].bm, bn = kTiles[tile].bn;
+    const int BK = (dtype == PT_FLOAT32 ? 16 : 32) * kTiles[tile].kmul;
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     bool vec_ok = aligned(a) && aligned(b);
     // vector (unchecked) loads need whole tiles, 16-byte aligned rows and

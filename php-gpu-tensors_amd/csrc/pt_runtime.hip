@@ -387,8 +387,8 @@ pt_status pt_rtc_compile(const char *source, const char *program_name,
         return fail(PT_ERR_COMPILE, "hiprtcCreateProgram failed");
     // No contraction: a fused a+b*c must round like the eager kernels
     // (fusion_precision.phpt:15-16); packed fp32 VALU ops stay disabled.
-    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off",
-                          "-std=c++17", "-mno-packed-fp32-ops"};
+    const char *opts[] = {"--offload-arch=gfx950", "-O3",      "-ffp-contract=off", "-std=c++17",
+                          "-Xclang",               "-target-feature", "-Xclang",           "-packed-fp32-ops"};
     hiprtcResult rc = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
     if (rc != HIPRTC_SUCCESS) {
         size_t n = 0;
@@ -444,8 +444,6 @@ pt_status pt_graph_begin_capture(pt_stream_t stream)
 {
     PT_TRY(ensure_init());
     hipStream_t s = stream_of(stream);
-    if (s == g_stream)
-        return fail(PT_ERR_INVALID, "graph capture needs a private stream");
     return check_hip(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal),
                      "hipStreamBeginCapture");
 }

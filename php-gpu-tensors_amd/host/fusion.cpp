@@ -1,0 +1,1329 @@
+// Fusion compiler of the host runtime, re-targeted at gfx950: capture of a
+// callback into a DAG (src/fusion_capture.c), plan building with the
+// reference's inline-cost cut rule (src/fusion_plan.c:39-100, budget 32),
+// HIP C++ code generation (replacing src/fusion_codegen.c's CUDA text),
+// hipRTC compilation with a source-keyed module cache (src/fusion_cache.c)
+// and replay, optionally through a captured HIP graph
+// (src/fusion_execute.c:385-598).
+//
+// Generated kernels evaluate every fused root for a contiguous range of
+// output elements.  When every leaf's address is an affine function of the
+// output coordinates (elementwise ops, broadcasting, transposed / sliced
+// leaves) the kernel walks the output four elements at a time: the
+// coordinates are decoded once per group, unit-stride leaves load 16-byte
+// vectors, zero-stride leaves load one scalar, and roots store 16-byte
+// vectors.  Other graphs (reshaped intermediates) use per-node index
+// functions with scalar accesses.  Node arithmetic matches the eager
+// kernels exactly: operands converted to the node dtype (float for
+// f16/bf16, rounded back after every node), no contraction (-ffp-contract=off),
+// the same device libm.
+#include "phpt_host.h"
+#include "runtime.hpp"
+
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+
+#include <algorithm>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <sstream>
+#include <unordered_map>
+
+namespace phpt {
+
+static constexpr int kKernelBudget = 32;  // FUSION_KERNEL_BUDGET, fusion_internal.h:18
+static constexpr int kMaxNodes = 4096;
+
+// ------------------------------------------------------------------- scope
+struct Scope {
+    std::vector<TensorP> recorded;
+    std::vector<TensorP> inputs;
+    bool compiling = false;
+};
+static thread_local Scope *t_scope = nullptr;
+
+bool fusion_active() { return t_scope != nullptr; }
+
+static TensorP record_node(std::shared_ptr<FusionNode> node, const int *shape, int ndims, int dtype)
+{
+    if (t_scope->recorded.size() >= (size_t)kMaxNodes) {
+        set_invalid("Fusion graph exceeds %d nodes", kMaxNodes);
+        return nullptr;
+    }
+    TensorP t = make_meta(shape, ndims, dtype);
+    if (!t) return nullptr;
+    t->node = node;
+    t_scope->recorded.push_back(t);
+    return t;
+}
+
+TensorP fusion_record(NodeKind kind, int op, std::vector<TensorP> inputs, const int *shape,
+                      int ndims, int dtype)
+{
+    auto n = std::make_shared<FusionNode>();
+    n->kind = kind;
+    n->op = op;
+    n->inputs = std::move(inputs);
+    return record_node(n, shape, ndims, dtype);
+}
+
+TensorP fusion_record_scalar(const TensorP &a, const Scalar &s, int op, bool reverse, int dtype)
+{
+    auto n = std::make_shared<FusionNode>();
+    n->kind = N_SCALAR;
+    n->op = op;
+    n->inputs = {a};
+    n->scalar = s;
+    n->reverse = reverse;
+    return record_node(n, a->shape, a->ndims, dtype);
+}
+
+TensorP fusion_record_view(const TensorP &a, const int *shape, const size_t *strides, int ndims,
+                           size_t offset)
+{
+    auto n = std::make_shared<FusionNode>();
+    n->kind = N_VIEW;
+    n->inputs = {a};
+    for (int d = 0; d < ndims; d++) n->view_strides[d] = strides[d];
+    n->view_offset = offset;
+    return record_node(n, shape, ndims, a->dtype);
+}
+
+TensorP fusion_record_native(const NativeSpec &spec, std::vector<TensorP> inputs, const int *shape,
+                             int ndims, int dtype)
+{
+    auto n = std::make_shared<FusionNode>();
+    n->kind = N_NATIVE;
+    n->native = spec;
+    n->inputs = std::move(inputs);
+    return record_node(n, shape, ndims, dtype);
+}
+
+// ------------------------------------------------------------------ plan
+enum ItemKind { IT_CONST = 0, IT_INPUT, IT_ELEM, IT_NATIVE };
+
+struct Item {
+    TensorP t;
+    int kind = IT_CONST;
+    int input_index = -1;
+    std::vector<int> args;
+    int cost = 0;
+    bool cut = false;       // materialized
+    bool output = false;
+    const char *reason = nullptr;
+};
+
+struct LeafMap {
+    bool affine = false;
+    long long offset = 0;              // element offset from the leaf base
+    long long stride[kMaxDims] = {0};  // per output coordinate
+};
+
+struct Kernel {
+    std::string name;
+    std::vector<int> roots;
+    std::vector<int> leaves;      // items read through pointers
+    int shape[kMaxDims] = {0};
+    int ndims = 0;
+    size_t total = 0;
+    bool affine = false;          // vectorizable (affine leaf maps)
+    std::vector<LeafMap> leaf_maps;
+    std::vector<bool> leaf_vec;   // leaf read as 4-vectors in the vector kernel
+    pt_function_t fn_vec = nullptr;
+    pt_function_t fn_scalar = nullptr;
+};
+
+struct Step {
+    bool native = false;
+    int kernel = -1;
+    int item = -1;
+};
+
+struct Plan {
+    std::vector<Item> items;
+    std::vector<Kernel> kernels;
+    std::vector<Step> steps;
+    std::vector<int> outputs;        // item index per output
+    std::vector<TensorP> input_examples;
+    std::string source;
+    pt_module_t module = nullptr;
+    bool cache_hit = false;
+    bool use_graph = false;
+    bool graph_compatible = true;
+    const char *incompatibility = nullptr;
+    pt_graph_t graph = nullptr;
+    std::vector<void *> graph_ptrs;  // pointers the captured graph was built with
+    // buffer reuse: item index -> storage kept between runs
+    std::unordered_map<int, std::shared_ptr<Storage>> cache;
+    // statistics (FusionGraph::getStats, fusion.c:723-772)
+    size_t executions = 0, graph_launches = 0, buffer_reuses = 0, tensor_allocations = 0;
+    size_t synchronizations = 0;
+    bool profiling = false;
+    size_t profiled = 0;
+    uint64_t bind_ns = 0, execute_ns = 0, collect_ns = 0;
+    bool pending = false;
+    pt_event_t done = nullptr;
+    std::vector<TensorP> pending_values;
+};
+
+static bool is_elementwise(const FusionNode &n)
+{
+    return n.kind == N_BINARY || n.kind == N_SCALAR || n.kind == N_UNARY || n.kind == N_CAST ||
+           n.kind == N_WHERE || n.kind == N_VIEW;
+}
+
+static int collect(Plan &p, const TensorP &t, std::map<const Tensor *, int> &index)
+{
+    auto it = index.find(t.get());
+    if (it != index.end()) return it->second;
+    Item item;
+    item.t = t;
+    if (t->node && t->node->kind == N_INPUT) {
+        item.kind = IT_INPUT;
+        item.input_index = t->node->input_index;
+    } else if (!t->node || t->storage) {
+        item.kind = IT_CONST;
+    } else {
+        for (const TensorP &in : t->node->inputs) item.args.push_back(collect(p, in, index));
+        item.kind = is_elementwise(*t->node) ? IT_ELEM : IT_NATIVE;
+    }
+    int id = (int)p.items.size();
+    p.items.push_back(item);
+    index[t.get()] = id;
+    Item &me = p.items[id];
+    // cost model (fusion_plan.c:39-100)
+    if (me.kind == IT_ELEM) {
+        const FusionNode &n = *t->node;
+        int base = n.kind == N_UNARY ? 4 : n.kind == N_WHERE ? 3 : n.kind == N_VIEW ? 2
+                 : n.op == PT_OP_POW ? 7 : 1;
+        if (t->dtype == PT_FLOAT64) base *= 2;
+        int cost = base;
+        for (int a : me.args)
+            if (p.items[a].kind == IT_ELEM && !p.items[a].cut) cost += p.items[a].cost;
+        if (cost > kKernelBudget) {
+            for (int a : me.args)
+                if (p.items[a].kind == IT_ELEM && p.items[a].cost) {
+                    p.items[a].cut = true;
+                    p.items[a].reason = "expression-cost";
+                }
+            cost = base;
+        }
+        me.cost = cost;
+    } else if (me.kind == IT_NATIVE) {
+        me.cut = true;
+        me.reason = "native";
+        for (int a : me.args)
+            if (p.items[a].kind == IT_ELEM) {
+                p.items[a].cut = true;
+                if (!p.items[a].reason) p.items[a].reason = "native-input";
+            }
+    }
+    return id;
+}
+
+// ------------------------------------------------------------ leaf maps
+// Affine map of item `id` evaluated at output coordinates: element offset
+// (relative to the leaf's base pointer) = off + sum c_d * st[d] over the
+// kernel's output dims.  `st` expresses the item's *logical* coordinates
+// in output coordinates, then leaf strides are applied.
+struct CoordMap {
+    // item coordinate k = sum over output dims d of coef[k][d] * c_d + base[k]
+    int nd_item = 0;
+    long long coef[kMaxDims][kMaxDims];
+    long long base[kMaxDims];
+};
+
+static CoordMap identity_map(int nd)
+{
+    CoordMap m;
+    m.nd_item = nd;
+    for (int k = 0; k < nd; k++) {
+        for (int d = 0; d < nd; d++) m.coef[k][d] = k == d ? 1 : 0;
+        m.base[k] = 0;
+    }
+    return m;
+}
+
+// operand of a broadcasting node: align trailing dims, extent-1 dims pinned to 0
+static CoordMap broadcast_child(const CoordMap &parent, const Tensor &parent_t, const Tensor &child, int nd_out)
+{
+    CoordMap m;
+    m.nd_item = child.ndims;
+    int off = parent_t.ndims - child.ndims;
+    for (int k = 0; k < child.ndims; k++) {
+        int pk = k + off;
+        for (int d = 0; d < nd_out; d++) m.coef[k][d] = child.shape[k] == 1 ? 0 : parent.coef[pk][d];
+        m.base[k] = child.shape[k] == 1 ? 0 : parent.base[pk];
+    }
+    return m;
+}
+
+struct Codegen {
+    Plan &p;
+    Kernel &k;
+    std::ostringstream &os;
+    std::map<int, int> leaf_slot;  // item -> leaf parameter index
+};
+
+static const char *ctype(int dt)
+{
+    switch (dt) {
+    case PT_FLOAT32: case PT_FLOAT16: case PT_BFLOAT16: return "float";
+    case PT_FLOAT64: return "double";
+    case PT_INT8: return "signed char";
+    case PT_INT16: return "short";
+    case PT_INT32: return "int";
+    case PT_INT64: return "long long";
+    case PT_UINT8: return "unsigned char";
+    case PT_UINT16: return "unsigned short";
+    case PT_UINT32: return "unsigned int";
+    case PT_UINT64: return "unsigned long long";
+    case PT_BOOL: return "bool";
+    default: return "float";
+    }
+}
+
+static const char *storage_type(int dt)
+{
+    switch (dt) {
+    case PT_FLOAT16: case PT_BFLOAT16: return "unsigned short";
+    case PT_BOOL: return "unsigned char";
+    default: return ctype(dt);
+    }
+}
+
+// Read of raw storage value `expr` of dtype dt as its compute type.
+static std::string load_conv(int dt, const std::string &expr)
+{
+    if (dt == PT_FLOAT16) return "pt_h2f(" + expr + ")";
+    if (dt == PT_BFLOAT16) return "pt_b2f(" + expr + ")";
+    if (dt == PT_BOOL) return "(" + expr + "!=0)";
+    return expr;
+}
+
+// Conversion of a compute-type value to storage of dtype dt.
+static std::string store_conv(int dt, const std::string &expr)
+{
+    if (dt == PT_FLOAT16) return "pt_f2h(" + expr + ")";
+    if (dt == PT_BFLOAT16) return "pt_f2b(" + expr + ")";
+    if (dt == PT_BOOL) return "(unsigned char)((" + expr + ")!=0)";
+    return expr;
+}
+
+static std::string scalar_literal(const Scalar &s)
+{
+    char buf[96];
+    switch (s.dtype) {
+    case PT_FLOAT64: {
+        uint64_t bits;
+        memcpy(&bits, &s.f, 8);
+        snprintf(buf, sizeof(buf), "__longlong_as_double(0x%llxLL)", (unsigned long long)bits);
+        break;
+    }
+    case PT_FLOAT32: case PT_FLOAT16: case PT_BFLOAT16: {
+        float f = (float)s.f;
+        uint32_t bits;
+        memcpy(&bits, &f, 4);
+        snprintf(buf, sizeof(buf), "__uint_as_float(0x%xu)", bits);
+        break;
+    }
+    case PT_BOOL: snprintf(buf, sizeof(buf), "%s", s.u ? "true" : "false"); break;
+    case PT_UINT8: case PT_UINT16: case PT_UINT32: case PT_UINT64:
+        snprintf(buf, sizeof(buf), "%lluULL", (unsigned long long)s.u);
+        break;
+    default: snprintf(buf, sizeof(buf), "(long long)%lldLL", (long long)s.i); break;
+    }
+    return buf;
+}
+
+static const char *math_name(int op)
+{
+    switch (op) {
+    case PT_OP_EXP: return "exp";
+    case PT_OP_EXPM1: return "expm1";
+    case PT_OP_EXP2: return "exp2";
+    case PT_OP_LOG: return "log";
+    case PT_OP_LOG1P: return "log1p";
+    case PT_OP_LOG2: return "log2";
+    case PT_OP_LOG10: return "log10";
+    case PT_OP_SQRT: return "sqrt";
+    case PT_OP_SIN: return "sin";
+    case PT_OP_COS: return "cos";
+    case PT_OP_TAN: return "tan";
+    case PT_OP_ASIN: return "asin";
+    case PT_OP_ACOS: return "acos";
+    case PT_OP_ATAN: return "atan";
+    case PT_OP_SINH: return "sinh";
+    case PT_OP_COSH: return "cosh";
+    case PT_OP_TANH: return "tanh";
+    case PT_OP_FLOOR: return "floor";
+    case PT_OP_CEIL: return "ceil";
+    case PT_OP_ROUND: return "round";
+    default: return nullptr;
+    }
+}
+
+// Expression of node `id` (compute type of its dtype) given operand
+// expressions; mirrors the eager kernels' bin_op / unary rules.
+static std::string node_expr(const Plan &p, int id, const std::vector<std::string> &a)
+{
+    const Item &it = p.items[id];
+    const Tensor &t = *it.t;
+    const FusionNode &n = *t.node;
+    std::string T = ctype(t.dtype);
+    bool int_out = !is_floating(t.dtype) && t.dtype != PT_BOOL;
+    auto cast = [&](const std::string &e) { return "static_cast<" + T + ">(" + e + ")"; };
+    std::string r;
+    switch (n.kind) {
+    case N_CAST:
+        if (t.dtype == PT_BOOL) r = "(" + a[0] + "!=0)";
+        else r = cast(a[0]);
+        break;
+    case N_VIEW: r = a[0]; break;
+    case N_WHERE: r = "((" + a[0] + ")!=0?" + cast(a[1]) + ":" + cast(a[2]) + ")"; break;
+    case N_UNARY: {
+        std::string x = cast(a[0]);
+        if (n.op == PT_OP_NEG) r = "(-" + x + ")";
+        else if (n.op == PT_OP_ABS) r = "(" + x + "<0?-" + x + ":" + x + ")";
+        else if (int_out && (n.op == PT_OP_FLOOR || n.op == PT_OP_CEIL || n.op == PT_OP_ROUND)) r = x;
+        else if (int_out || t.dtype == PT_BOOL)
+            r = cast(std::string(math_name(n.op)) + "f(static_cast<float>(" + x + "))");
+        else
+            r = std::string(math_name(n.op)) + (t.dtype == PT_FLOAT64 ? "" : "f") + "(" + x + ")";
+        break;
+    }
+    case N_BINARY:
+    case N_SCALAR: {
+        std::string x, y;
+        if (n.kind == N_BINARY) {
+            x = cast(a[0]);
+            y = cast(a[1]);
+        } else {
+            std::string sv = cast(scalar_literal(n.scalar));
+            x = n.reverse ? sv : cast(a[0]);
+            y = n.reverse ? cast(a[0]) : sv;
+        }
+        switch (n.op) {
+        case PT_OP_ADD: r = "(" + x + "+" + y + ")"; break;
+        case PT_OP_SUB: r = "(" + x + "-" + y + ")"; break;
+        case PT_OP_MUL: r = "(" + x + "*" + y + ")"; break;
+        case PT_OP_DIV:
+            r = int_out ? "(" + y + "==0?" + cast("0") + ":" + x + "/" + y + ")" : "(" + x + "/" + y + ")";
+            break;
+        case PT_OP_POW: r = (int_out ? "pt_powi(" : "pt_pow(") + x + "," + y + ")"; break;
+        case PT_OP_MAXIMUM: r = "(" + x + ">" + y + "?" + x + ":" + y + ")"; break;
+        case PT_OP_MINIMUM: r = "(" + x + "<" + y + "?" + x + ":" + y + ")"; break;
+        case PT_OP_GT: r = "(" + x + ">" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        case PT_OP_LT: r = "(" + x + "<" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        case PT_OP_EQ: r = "(" + x + "==" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        case PT_OP_NE: r = "(" + x + "!=" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        case PT_OP_GE: r = "(" + x + ">=" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        case PT_OP_LE: r = "(" + x + "<=" + y + "?" + cast("1") + ":" + cast("0") + ")"; break;
+        default: r = x; break;
+        }
+        break;
+    }
+    default: r = "0"; break;
+    }
+    // low-precision nodes round after every op (eager kernels store them)
+    if (t.dtype == PT_FLOAT16) r = "pt_h2f(pt_f2h(" + r + "))";
+    else if (t.dtype == PT_BFLOAT16) r = "pt_b2f(pt_f2b(" + r + "))";
+    return r;
+}
+
+static bool is_leaf(const Plan &p, const Kernel &k, int id)
+{
+    const Item &it = p.items[id];
+    if (it.kind != IT_ELEM) return true;
+    if (!it.cut) return false;
+    return std::find(k.roots.begin(), k.roots.end(), id) == k.roots.end();
+}
+
+// Gather leaves of a kernel and decide whether every leaf map is affine.
+static void gather(const Plan &p, Kernel &k, int id, const CoordMap &cm, bool &affine,
+                   std::vector<std::pair<int, CoordMap>> &uses)
+{
+    const Item &it = p.items[id];
+    if (is_leaf(p, k, id)) {
+        uses.push_back({id, cm});
+        if (std::find(k.leaves.begin(), k.leaves.end(), id) == k.leaves.end()) k.leaves.push_back(id);
+        return;
+    }
+    const Tensor &t = *it.t;
+    const FusionNode &n = *t.node;
+    if (n.kind == N_VIEW) {
+        // source linear index = off + sum coord_d * view_stride_d; affine in
+        // the source's coordinates only when the source is 1-D or the view
+        // strides decompose; keep the general path for these.
+        affine = false;
+        CoordMap dummy = identity_map(p.items[it.args[0]].t->ndims);
+        gather(p, k, it.args[0], dummy, affine, uses);
+        return;
+    }
+    for (int a : it.args) {
+        const Tensor &c = *p.items[a].t;
+        gather(p, k, a, broadcast_child(cm, t, c, k.ndims), affine, uses);
+    }
+}
+
+// ------------------------------------------------------ code generation
+static void emit_prelude(std::ostringstream &os)
+{
+    os << "#include <hip/hip_runtime.h>\n"
+          "__device__ __forceinline__ float pt_b2f(unsigned short b){return __uint_as_float(((unsigned)b)<<16);}\n"
+          "__device__ __forceinline__ unsigned short pt_f2b(float f){unsigned u=__float_as_uint(f);"
+          "if((u&0x7f800000u)==0x7f800000u&&(u&0x7fffffu))return (unsigned short)((u>>16)|0x40u);"
+          "return (unsigned short)((u+0x7fffu+((u>>16)&1u))>>16);}\n"
+          "__device__ __forceinline__ float pt_h2f(unsigned short h){return (float)__builtin_bit_cast(_Float16,h);}\n"
+          "__device__ __forceinline__ unsigned short pt_f2h(float f){unsigned u=__float_as_uint(f);"
+          "if((u&0x7f800000u)==0x7f800000u&&(u&0x7fffffu)){unsigned p=(u&0x7fffffu)>>13;if(!p)p=1;"
+          "return (unsigned short)(((u>>16)&0x8000u)|0x7c00u|p);}return __builtin_bit_cast(unsigned short,(_Float16)f);}\n"
+          "template<typename T>__device__ __forceinline__ T pt_ipow(T b,int e){T r=(T)1;while(e>0){if(e&1)r=r*b;b=b*b;e>>=1;}return r;}\n"
+          "__device__ __forceinline__ float pt_pow(float a,float b){if(b==floorf(b)){int e=(int)b;"
+          "if(e==0)return 1.0f;if(e==1)return a;if(e==2)return a*a;if(e==3)return a*a*a;"
+          "if(e<0)return 1.0f/pt_ipow(a,-e);return pt_ipow(a,e);}return powf(a,b);}\n"
+          "__device__ __forceinline__ double pt_pow(double a,double b){if(b==floor(b)){int e=(int)b;"
+          "if(e==0)return 1.0;if(e==1)return a;if(e==2)return a*a;if(e==3)return a*a*a;"
+          "if(e<0)return 1.0/pt_ipow(a,-e);return pt_ipow(a,e);}return pow(a,b);}\n"
+          "template<typename T>__device__ __forceinline__ T pt_powi(T a,T b){int e=(int)b;"
+          "if(e==0)return (T)1;if(e==1)return a;if(e==2)return a*a;if(e==3)return a*a*a;"
+          "if(e<0)return (T)0;return pt_ipow(a,e);}\n";
+}
+
+// General path: one device function per node, evaluated at the node's own
+// linear index (as the reference codegen does), scalar accesses.
+static void emit_general(Plan &p, Kernel &k, std::ostringstream &os)
+{
+    std::vector<char> emitted(p.items.size(), 0);
+    std::string params;
+    for (size_t l = 0; l < k.leaves.size(); l++) params += "const void* __restrict__ p" + std::to_string(l) + ",";
+    std::string args;
+    for (size_t l = 0; l < k.leaves.size(); l++) args += "p" + std::to_string(l) + ",";
+    std::function<void(int)> emit = [&](int id) {
+        if (emitted[id]) return;
+        emitted[id] = 1;
+        const Item &it = p.items[id];
+        const Tensor &t = *it.t;
+        std::string fname = k.name + "_n" + std::to_string(id);
+        bool leaf = is_leaf(p, k, id);
+        if (!leaf)
+            for (int a : it.args) emit(a);
+        os << "__device__ __forceinline__ " << ctype(t.dtype) << " " << fname << "(" << params
+           << "unsigned long long i){\n";
+        if (leaf) {
+            int slot = (int)(std::find(k.leaves.begin(), k.leaves.end(), id) - k.leaves.begin());
+            // leaves read with their own strides (constants, inputs) or
+            // contiguously (materialized buffers)
+            bool own = it.kind == IT_CONST || it.kind == IT_INPUT;
+            const Tensor &src = (it.kind == IT_INPUT) ? *p.input_examples[it.input_index] : t;
+            os << "unsigned long long o=0;\n";
+            unsigned long long div = 1;
+            for (int d = t.ndims - 1; d >= 0; d--) {
+                unsigned long long st = own ? (unsigned long long)src.strides[d] : div;
+                if (t.shape[d] > 1)
+                    os << "o+=((i/" << div << "ULL)%" << t.shape[d] << "ULL)*" << st << "ULL;\n";
+                div *= (unsigned long long)(t.shape[d] ? t.shape[d] : 1);
+            }
+            os << "return " << load_conv(t.dtype, std::string("static_cast<const ") + storage_type(t.dtype) +
+                                                       "*>(p" + std::to_string(slot) + ")[o]")
+               << ";}\n";
+            return;
+        }
+        const FusionNode &n = *t.node;
+        std::vector<std::string> ops;
+        int c = 0;
+        for (int a : it.args) {
+            const Tensor &ct = *p.items[a].t;
+            std::string var = "i" + std::to_string(c++);
+            if (n.kind == N_VIEW) {
+                os << "unsigned long long " << var << "=" << n.view_offset << "ULL;\n";
+                unsigned long long div = 1;
+                for (int d = t.ndims - 1; d >= 0; d--) {
+                    if (t.shape[d] > 1)
+                        os << var << "+=((i/" << div << "ULL)%" << t.shape[d] << "ULL)*" << n.view_strides[d]
+                           << "ULL;\n";
+                    div *= (unsigned long long)(t.shape[d] ? t.shape[d] : 1);
+                }
+            } else {
+                // broadcast projection of the output index onto the operand
+                os << "unsigned long long " << var << "=0;\n";
+                unsigned long long div = 1, st = 1;
+                int off = t.ndims - ct.ndims;
+                for (int d = t.ndims - 1; d >= 0; d--) {
+                    int cd = d - off;
+                    if (cd >= 0) {
+                        if (ct.shape[cd] != 1 && t.shape[d] > 1)
+                            os << var << "+=((i/" << div << "ULL)%" << t.shape[d] << "ULL)*" << st << "ULL;\n";
+                        st *= (unsigned long long)(ct.shape[cd] ? ct.shape[cd] : 1);
+                    }
+                    div *= (unsigned long long)(t.shape[d] ? t.shape[d] : 1);
+                }
+            }
+            os << ctype(ct.dtype) << " v" << (c - 1) << "=" << k.name << "_n" << a << "(" << args << var << ");\n";
+            ops.push_back("v" + std::to_string(c - 1));
+        }
+        os << "return " << node_expr(p, id, ops) << ";}\n";
+    };
+    for (int r : k.roots) emit(r);
+    os << "extern \"C\" __global__ void " << k.name << "_s(" << params;
+    for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
+    os << "){for(unsigned long long i=(unsigned long long)blockIdx.x*blockDim.x+threadIdx.x;i<" << k.total
+       << "ULL;i+=(unsigned long long)blockDim.x*gridDim.x){\n";
+    for (size_t r = 0; r < k.roots.size(); r++) {
+        int id = k.roots[r];
+        const Tensor &t = *p.items[id].t;
+        os << "static_cast<" << storage_type(t.dtype) << "*>(out" << r << ")[i]="
+           << store_conv(t.dtype, k.name + "_n" + std::to_string(id) + "(" + args + "i)") << ";\n";
+    }
+    os << "}}\n";
+}
+
+// Vector path: coordinates decoded once per group of 4 output elements.
+static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
+{
+    std::string params;
+    for (size_t l = 0; l < k.leaves.size(); l++) params += "const void* __restrict__ p" + std::to_string(l) + ",";
+    os << "extern \"C\" __global__ void " << k.name << "_v(" << params;
+    for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
+    const int nd = k.ndims;
+    os << "){\nconst unsigned long long n4=" << k.total / 4 << "ULL;\n"
+       << "for(unsigned long long g=(unsigned long long)blockIdx.x*blockDim.x+threadIdx.x;g<n4;"
+          "g+=(unsigned long long)blockDim.x*gridDim.x){\n"
+       << "const unsigned long long i0=g*4ULL;\n";
+    // coordinates of element i0
+    unsigned long long div = 1;
+    for (int d = nd - 1; d >= 0; d--) {
+        os << "const unsigned long long c" << d << "=(i0/" << div << "ULL)%" << k.shape[d] << "ULL;\n";
+        div *= (unsigned long long)k.shape[d];
+    }
+    // leaf loads: L<slot>_<j>
+    for (size_t l = 0; l < k.leaves.size(); l++) {
+        const LeafMap &m = k.leaf_maps[l];
+        int id = k.leaves[l];
+        const Tensor &t = *p.items[id].t;
+        std::string st = storage_type(t.dtype);
+        os << "const unsigned long long o" << l << "=" << m.offset << "ULL";
+        for (int d = 0; d < nd; d++)
+            if (m.stride[d]) os << "+c" << d << "*" << m.stride[d] << "ULL";
+        os << ";\n";
+        std::string base = "static_cast<const " + st + "*>(p" + std::to_string(l) + ")";
+        long long inner = nd ? m.stride[nd - 1] : 0;
+        if (inner == 0) {
+            os << "const " << ctype(t.dtype) << " L" << l << "=" << load_conv(t.dtype, base + "[o" + std::to_string(l) + "]")
+               << ";\n";
+            for (int j = 0; j < 4; j++)
+                os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "=L" << l << ";\n";
+        } else if (inner == 1 && k.leaf_vec[l]) {
+            size_t es = dtype_size(t.dtype);
+            if (es == 4) {
+                os << "const uint4 R" << l << "=*reinterpret_cast<const uint4*>(" << base << "+o" << l << ");\n";
+                const char *f[4] = {"x", "y", "z", "w"};
+                for (int j = 0; j < 4; j++) {
+                    std::string raw = std::string("R") + std::to_string(l) + "." + f[j];
+                    std::string v = t.dtype == PT_FLOAT32 ? "__uint_as_float(" + raw + ")"
+                                  : "static_cast<" + std::string(ctype(t.dtype)) + ">(" + raw + ")";
+                    os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "=" << v << ";\n";
+                }
+            } else {
+                for (int j = 0; j < 4; j++)
+                    os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "="
+                       << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j) + "]") << ";\n";
+            }
+        } else {
+            for (int j = 0; j < 4; j++)
+                os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "="
+                   << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j * inner) + "ULL]")
+                   << ";\n";
+        }
+    }
+    // per element j: evaluate the roots' expression trees
+    for (int j = 0; j < 4; j++) {
+        std::map<int, std::string> val;
+        std::function<std::string(int)> ev = [&](int id) -> std::string {
+            auto it = val.find(id);
+            if (it != val.end()) return it->second;
+            if (is_leaf(p, k, id)) {
+                int slot = (int)(std::find(k.leaves.begin(), k.leaves.end(), id) - k.leaves.begin());
+                return val[id] = "L" + std::to_string(slot) + "_" + std::to_string(j);
+            }
+            std::vector<std::string> ops;
+            for (int a : p.items[id].args) ops.push_back(ev(a));
+            std::string name = "e" + std::to_string(id) + "_" + std::to_string(j);
+            os << "const " << ctype(p.items[id].t->dtype) << " " << name << "=" << node_expr(p, id, ops) << ";\n";
+            return val[id] = name;
+        };
+        for (int r : k.roots) ev(r);
+        for (size_t r = 0; r < k.roots.size(); r++) {
+            int id = k.roots[r];
+            os << "const " << ctype(p.items[id].t->dtype) << " r" << r << "_" << j << "=" << val[id] << ";\n";
+        }
+    }
+    for (size_t r = 0; r < k.roots.size(); r++) {
+        const Tensor &t = *p.items[k.roots[r]].t;
+        std::string st = storage_type(t.dtype);
+        if (t.dtype == PT_FLOAT32) {
+            os << "*reinterpret_cast<float4*>(static_cast<float*>(out" << r << ")+i0)=make_float4(r" << r
+               << "_0,r" << r << "_1,r" << r << "_2,r" << r << "_3);\n";
+        } else {
+            for (int j = 0; j < 4; j++)
+                os << "static_cast<" << st << "*>(out" << r << ")[i0+" << j << "]="
+                   << store_conv(t.dtype, "r" + std::to_string(r) + "_" + std::to_string(j)) << ";\n";
+        }
+    }
+    os << "}}\n";
+}
+
+// ------------------------------------------------------------ module cache
+struct ModuleCache {
+    std::mutex mu;
+    std::unordered_map<std::string, pt_module_t> modules;
+    std::vector<std::string> order;
+    size_t hits = 0, misses = 0, evictions = 0;
+};
+static ModuleCache g_cache;
+static const size_t kCacheEntries = 16;  // fusion_cache.c: 16-entry LRU
+
+static pt_module_t load_module(const std::string &src, bool &hit)
+{
+    std::lock_guard<std::mutex> lock(g_cache.mu);
+    auto it = g_cache.modules.find(src);
+    if (it != g_cache.modules.end()) {
+        hit = true;
+        g_cache.hits++;
+        auto pos = std::find(g_cache.order.begin(), g_cache.order.end(), src);
+        if (pos != g_cache.order.end()) {
+            g_cache.order.erase(pos);
+            g_cache.order.push_back(src);
+        }
+        return it->second;
+    }
+    hit = false;
+    g_cache.misses++;
+    pt_module_t m = nullptr;
+    static char log[8192];
+    if (!check_status(pt_rtc_compile(src.c_str(), "fusion.hip", &m, log, sizeof(log)), "Fusion compilation failed"))
+        return nullptr;
+    // modules stay loaded while plans may use them; eviction only drops
+    // the cache entry (compiled graphs keep their module handle)
+    g_cache.modules[src] = m;
+    g_cache.order.push_back(src);
+    while (g_cache.order.size() > kCacheEntries) {
+        g_cache.modules.erase(g_cache.order.front());
+        g_cache.order.erase(g_cache.order.begin());
+        g_cache.evictions++;
+    }
+    return m;
+}
+
+// ------------------------------------------------------------ plan build
+static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<TensorP> &inputs)
+{
+    auto *p = new Plan();
+    p->input_examples = inputs;
+    std::map<const Tensor *, int> index;
+    for (const TensorP &r : roots) {
+        int id = collect(*p, r, index);
+        p->items[id].output = true;
+        p->outputs.push_back(id);
+    }
+    for (int id : p->outputs)
+        if (p->items[id].kind == IT_ELEM) p->items[id].cut = true;
+    // steps in item (topological) order; elementwise roots with the same
+    // shape that do not depend on each other share one kernel
+    Kernel cur;
+    auto depends = [&](int id, const std::vector<int> &set) {
+        std::function<bool(int)> walk = [&](int x) -> bool {
+            if (std::find(set.begin(), set.end(), x) != set.end()) return true;
+            const Item &it = p->items[x];
+            if (it.kind != IT_ELEM) return false;
+            for (int a : it.args)
+                if (walk(a)) return true;
+            return false;
+        };
+        for (int a : p->items[id].args)
+            if (walk(a)) return true;
+        return false;
+    };
+    auto flush = [&]() {
+        if (cur.roots.empty()) return;
+        cur.name = "fk" + std::to_string(p->kernels.size());
+        Step st;
+        st.kernel = (int)p->kernels.size();
+        p->kernels.push_back(cur);
+        p->steps.push_back(st);
+        cur = Kernel();
+    };
+    for (int id = 0; id < (int)p->items.size(); id++) {
+        Item &it = p->items[id];
+        if (it.kind == IT_NATIVE) {
+            flush();
+            Step st;
+            st.native = true;
+            st.item = id;
+            p->steps.push_back(st);
+        } else if (it.kind == IT_ELEM && it.cut) {
+            const Tensor &t = *it.t;
+            bool same = !cur.roots.empty() && cur.ndims == t.ndims &&
+                        std::equal(t.shape, t.shape + t.ndims, cur.shape) && cur.roots.size() < 4;
+            if (!same || depends(id, cur.roots)) flush();
+            if (cur.roots.empty()) {
+                cur.ndims = t.ndims;
+                for (int d = 0; d < t.ndims; d++) cur.shape[d] = t.shape[d];
+                cur.total = t.numel();
+            }
+            cur.roots.push_back(id);
+        }
+    }
+    flush();
+    // leaves, maps and source
+    std::ostringstream os;
+    emit_prelude(os);
+    for (Kernel &k : p->kernels) {
+        bool affine = true;
+        std::vector<std::pair<int, CoordMap>> uses;
+        for (int r : k.roots) gather(*p, k, r, identity_map(k.ndims), affine, uses);
+        // a leaf used through two different maps keeps the general path
+        k.leaf_maps.assign(k.leaves.size(), LeafMap());
+        std::vector<bool> seen(k.leaves.size(), false);
+        for (auto &u : uses) {
+            int slot = (int)(std::find(k.leaves.begin(), k.leaves.end(), u.first) - k.leaves.begin());
+            const Item &it = p->items[u.first];
+            const Tensor &src = it.kind == IT_INPUT ? *p->input_examples[it.input_index] : *it.t;
+            bool own = it.kind == IT_CONST || it.kind == IT_INPUT;
+            size_t cstr[kMaxDims];
+            contiguous_strides(it.t->shape, it.t->ndims, cstr);
+            LeafMap m;
+            m.affine = true;
+            for (int kk = 0; kk < u.second.nd_item; kk++) {
+                long long s = own ? (long long)src.strides[kk] : (long long)cstr[kk];
+                m.offset += u.second.base[kk] * s;
+                for (int d = 0; d < k.ndims; d++) m.stride[d] += u.second.coef[kk][d] * s;
+            }
+            if (seen[slot] && memcmp(&k.leaf_maps[slot], &m, sizeof(m)) != 0) affine = false;
+            k.leaf_maps[slot] = m;
+            seen[slot] = true;
+        }
+        k.affine = affine && k.ndims > 0 && k.total % 4 == 0 && k.shape[k.ndims - 1] % 4 == 0;
+        k.leaf_vec.assign(k.leaves.size(), false);
+        if (k.affine) {
+            for (size_t l = 0; l < k.leaves.size(); l++) {
+                const LeafMap &m = k.leaf_maps[l];
+                const Tensor &lt = *p->items[k.leaves[l]].t;
+                bool v = m.stride[k.ndims - 1] == 1 && dtype_size(lt.dtype) == 4 && m.offset % 4 == 0;
+                for (int d = 0; d < k.ndims - 1 && v; d++) v = m.stride[d] % 4 == 0;
+                k.leaf_vec[l] = v;
+            }
+            emit_vector(*p, k, os);
+        }
+        emit_general(*p, k, os);
+    }
+    p->source = os.str();
+    // graph compatibility: every step can be captured except native steps
+    // whose kernels need host-side choices per call (none here) -- plans
+    // with views of intermediates still replay eagerly between kernels
+    return p;
+}
+
+// ------------------------------------------------------------ execution
+static uint64_t now_ns()
+{
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
+}
+
+// Storage for item `id` (materialized elementwise root): reuse the cached
+// buffer when nobody else holds it any more.
+static std::shared_ptr<Storage> buffer_for(Plan &p, int id, size_t bytes)
+{
+    auto it = p.cache.find(id);
+    if (it != p.cache.end() && it->second.use_count() == 1 && it->second->bytes >= bytes) {
+        p.buffer_reuses++;
+        return it->second;
+    }
+    auto st = std::make_shared<Storage>();
+    st->bytes = bytes;
+    if (!check_status(pt_alloc(&st->ptr, bytes ? bytes : 1, nullptr), "Fusion buffer allocation"))
+        return nullptr;
+    p.tensor_allocations++;
+    p.cache[id] = st;
+    return st;
+}
+
+static const void *leaf_ptr(const Plan &p, const std::vector<TensorP> &vals, int id)
+{
+    const TensorP &v = vals[id];
+    (void)p;
+    return v->data();
+}
+
+static bool launch_kernel(Plan &p, Kernel &k, std::vector<TensorP> &vals)
+{
+    std::vector<void *> ptrs;
+    bool vec_ok = k.affine && k.fn_vec;
+    for (size_t l = 0; l < k.leaves.size(); l++) {
+        const void *ptr = leaf_ptr(p, vals, k.leaves[l]);
+        ptrs.push_back(const_cast<void *>(ptr));
+        if (k.leaf_vec[l] && ((uintptr_t)ptr & 15)) vec_ok = false;
+    }
+    for (int r : k.roots) {
+        void *ptr = vals[r]->data();
+        ptrs.push_back(ptr);
+        if ((uintptr_t)ptr & 15) vec_ok = false;
+    }
+    if (!k.total) return true;
+    std::vector<void *> params;
+    for (void *&ptr : ptrs) params.push_back(&ptr);
+    size_t work = vec_ok ? k.total / 4 : k.total;
+    size_t blocks = (work + 255) / 256;
+    if (blocks > 256 * 32) blocks = 256 * 32;  // grid-stride beyond 32 workgroups per CU
+    return check_status(pt_launch(vec_ok ? k.fn_vec : k.fn_scalar, (unsigned)blocks, 256, params.data(),
+                                  nullptr),
+                        "Fusion kernel launch failed");
+}
+
+static bool run_steps(Plan &p, std::vector<TensorP> &vals)
+{
+    for (Step &st : p.steps) {
+        if (st.native) {
+            Item &it = p.items[st.item];
+            std::vector<TensorP> ins;
+            for (int a : it.args) ins.push_back(vals[a]);
+            TensorP out = native_execute(it.t->node->native, ins);
+            if (!out) return false;
+            vals[st.item] = out;
+        } else {
+            if (!launch_kernel(p, p.kernels[st.kernel], vals)) return false;
+        }
+    }
+    return true;
+}
+
+// Allocate materialized values for a run (outside graph capture).
+static bool prepare_values(Plan &p, std::vector<TensorP> &vals)
+{
+    for (Kernel &k : p.kernels)
+        for (int r : k.roots) {
+            const Tensor &t = *p.items[r].t;
+            auto st = buffer_for(p, r, t.numel() * dtype_size(t.dtype));
+            if (!st) return false;
+            TensorP v = make_meta(t.shape, t.ndims, t.dtype);
+            v->storage = st;
+            vals[r] = v;
+        }
+    return true;
+}
+
+static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<TensorP> &outs, bool wait)
+{
+    uint64_t t0 = now_ns();
+    std::vector<TensorP> vals(p.items.size());
+    for (size_t i = 0; i < p.items.size(); i++) {
+        Item &it = p.items[i];
+        if (it.kind == IT_CONST) {
+            if (it.t->lazy() && !fusion_materialize(it.t)) return false;
+            vals[i] = it.t;
+        } else if (it.kind == IT_INPUT) {
+            vals[i] = inputs[it.input_index];
+        }
+    }
+    if (!prepare_values(p, vals)) return false;
+    uint64_t t1 = now_ns();
+    bool graph_ok = p.use_graph && p.graph_compatible;
+    bool native_present = false;
+    for (Step &st : p.steps) native_present = native_present || st.native;
+    if (graph_ok && native_present) {
+        // native steps allocate their results; pre-run once eagerly so that
+        // their buffers come from the pool, then replay the whole plan from
+        // the graph only when every step is an elementwise kernel
+        graph_ok = false;
+    }
+    if (graph_ok) {
+        std::vector<void *> ptrs;
+        for (size_t i = 0; i < vals.size(); i++)
+            if (vals[i]) ptrs.push_back(vals[i]->data());
+        if (!p.graph || ptrs != p.graph_ptrs) {
+            if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
+            bool ok = run_steps(p, vals);
+            pt_status st = p.graph ? pt_graph_end_capture_update(nullptr, p.graph)
+                                   : pt_graph_end_capture(nullptr, &p.graph);
+            if (!ok) return false;
+            if (!check_status(st, "Graph instantiation failed")) return false;
+            p.graph_ptrs = ptrs;
+        }
+        if (!check_status(pt_graph_launch(p.graph, nullptr), "Graph launch failed")) return false;
+        p.graph_launches++;
+    } else {
+        if (!run_steps(p, vals)) return false;
+    }
+    if (wait) {
+        if (!check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed")) return false;
+        p.synchronizations++;
+    }
+    uint64_t t2 = now_ns();
+    outs.clear();
+    for (int id : p.outputs) {
+        TensorP v = vals[id];
+        // outputs are views of the value with the output's metadata
+        TensorP o = make_meta(p.items[id].t->shape, p.items[id].t->ndims, p.items[id].t->dtype);
+        o->storage = v->storage;
+        o->offset = v->offset;
+        for (int d = 0; d < o->ndims; d++) o->strides[d] = v->strides[d];
+        if (p.items[id].kind == IT_CONST || p.items[id].kind == IT_INPUT) o = materialize(v);
+        outs.push_back(o);
+    }
+    p.executions++;
+    if (p.profiling) {
+        uint64_t t3 = now_ns();
+        p.profiled++;
+        p.bind_ns += t1 - t0;
+        p.execute_ns += t2 - t1;
+        p.collect_ns += t3 - t2;
+    }
+    return true;
+}
+
+static bool compile_plan(Plan &p)
+{
+    if (p.kernels.empty()) return true;
+    p.module = load_module(p.source, p.cache_hit);
+    if (!p.module) return false;
+    for (Kernel &k : p.kernels) {
+        if (k.affine &&
+            !check_status(pt_module_function(p.module, (k.name + "_v").c_str(), &k.fn_vec), "Fusion kernel lookup"))
+            return false;
+        if (!check_status(pt_module_function(p.module, (k.name + "_s").c_str(), &k.fn_scalar), "Fusion kernel lookup"))
+            return false;
+    }
+    return true;
+}
+
+bool fusion_materialize(const TensorP &t)
+{
+    if (!t->lazy()) return true;
+    // evaluate the recorded subgraph producing `t` now (Fusion::run reads
+    // inside the callback), then keep `t` as a concrete value
+    Scope *saved = t_scope;
+    t_scope = nullptr;
+    std::unique_ptr<Plan> p(build_plan({t}, saved ? saved->inputs : std::vector<TensorP>()));
+    for (const Item &it : p->items)
+        if (it.kind == IT_INPUT) {
+            t_scope = saved;
+            set_invalid("Compiled Fusion inputs cannot be read during capture");
+            return false;
+        }
+    bool ok = compile_plan(*p);
+    std::vector<TensorP> outs;
+    if (ok) ok = execute(*p, {}, outs, false);
+    t_scope = saved;
+    if (!ok) return false;
+    t->storage = outs[0]->storage;
+    t->offset = outs[0]->offset;
+    for (int d = 0; d < t->ndims; d++) t->strides[d] = outs[0]->strides[d];
+    return true;
+}
+
+}  // namespace phpt
+
+// =================================================================== C API
+using namespace phpt;
+
+struct phpt_graph {
+    Plan *plan;
+};
+
+static phpt_tensor *wrap(const TensorP &t)
+{
+    if (!t) return nullptr;
+    auto *h = new phpt_tensor;
+    h->t = t;
+    return h;
+}
+
+static thread_local std::string t_text;
+
+extern "C" {
+
+int phpt_fusion_begin(int compiling)
+{
+    clear_error();
+    if (t_scope) {
+        set_invalid("Fusion scopes cannot be nested");
+        return -1;
+    }
+    t_scope = new Scope();
+    t_scope->compiling = compiling != 0;
+    return 0;
+}
+
+int phpt_fusion_active(void) { return fusion_active() ? 1 : 0; }
+
+void phpt_fusion_abort(void)
+{
+    delete t_scope;
+    t_scope = nullptr;
+}
+
+phpt_tensor *phpt_fusion_input(phpt_tensor *example, int index)
+{
+    clear_error();
+    if (!t_scope) {
+        set_invalid("No active Fusion scope");
+        return nullptr;
+    }
+    const TensorP &ex = example->t;
+    if (ex->lazy()) {
+        set_invalid("Fusion inputs must be materialized CudaArray values");
+        return nullptr;
+    }
+    auto n = std::make_shared<FusionNode>();
+    n->kind = N_INPUT;
+    n->input_index = index;
+    TensorP t = make_meta(ex->shape, ex->ndims, ex->dtype);
+    if (!t) return nullptr;
+    t->node = n;
+    if ((int)t_scope->inputs.size() <= index) t_scope->inputs.resize(index + 1);
+    t_scope->inputs[index] = ex;
+    t_scope->recorded.push_back(t);
+    return wrap(t);
+}
+
+phpt_graph *phpt_fusion_end(phpt_tensor **outputs, int count, int use_graph)
+{
+    clear_error();
+    if (!t_scope) {
+        set_invalid("No active Fusion scope");
+        return nullptr;
+    }
+    Scope *scope = t_scope;
+    t_scope = nullptr;
+    std::vector<TensorP> roots;
+    for (int i = 0; i < count; i++) roots.push_back(outputs[i]->t);
+    Plan *p = build_plan(roots, scope->inputs);
+    delete scope;
+    p->use_graph = use_graph != 0;
+    if (!compile_plan(*p)) {
+        delete p;
+        return nullptr;
+    }
+    auto *g = new phpt_graph;
+    g->plan = p;
+    return g;
+}
+
+int phpt_fusion_run_once(phpt_tensor **outputs, int count)
+{
+    clear_error();
+    if (!t_scope) {
+        set_invalid("No active Fusion scope");
+        return -1;
+    }
+    Scope *scope = t_scope;
+    t_scope = nullptr;
+    // roots: the returned values plus recorded values still referenced
+    // outside the scope (escaped through closures)
+    std::vector<TensorP> roots;
+    for (int i = 0; i < count; i++)
+        if (outputs[i]->t->lazy()) roots.push_back(outputs[i]->t);
+    for (const TensorP &t : scope->recorded)
+        if (t->lazy() && t.use_count() > 2 &&
+            std::find(roots.begin(), roots.end(), t) == roots.end())
+            roots.push_back(t);
+    int rc = 0;
+    if (!roots.empty()) {
+        std::unique_ptr<Plan> p(build_plan(roots, {}));
+        std::vector<TensorP> outs;
+        if (!compile_plan(*p) || !execute(*p, {}, outs, true)) {
+            rc = -1;
+        } else {
+            for (size_t i = 0; i < roots.size(); i++) {
+                roots[i]->storage = outs[i]->storage;
+                roots[i]->offset = outs[i]->offset;
+                for (int d = 0; d < roots[i]->ndims; d++) roots[i]->strides[d] = outs[i]->strides[d];
+                roots[i]->node.reset();
+            }
+        }
+    }
+    delete scope;
+    return rc;
+}
+
+static bool bind(Plan &p, phpt_tensor **inputs, int n, std::vector<TensorP> &out)
+{
+    if (n != (int)p.input_examples.size()) {
+        set_invalid("FusionGraph expects %zu inputs, %d given", p.input_examples.size(), n);
+        return false;
+    }
+    for (int i = 0; i < n; i++) {
+        const TensorP &ex = p.input_examples[i];
+        const TensorP &t = inputs[i]->t;
+        if (t->lazy()) {
+            set_invalid("FusionGraph inputs must be materialized");
+            return false;
+        }
+        bool same = t->dtype == ex->dtype && t->ndims == ex->ndims;
+        for (int d = 0; same && d < t->ndims; d++)
+            same = t->shape[d] == ex->shape[d] && (t->shape[d] == 1 || t->strides[d] == ex->strides[d]);
+        if (!same) {
+            set_invalid("FusionGraph input %d does not match the captured shape, dtype and strides", i);
+            return false;
+        }
+        out.push_back(t);
+    }
+    return true;
+}
+
+int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor **outputs, int noutputs)
+{
+    clear_error();
+    Plan &p = *g->plan;
+    if (p.pending) {
+        set_runtime("FusionGraph has a pending asynchronous replay; wait() first");
+        return -1;
+    }
+    std::vector<TensorP> ins, outs;
+    if (!bind(p, inputs, ninputs, ins)) return -1;
+    if (!execute(p, ins, outs, true)) return -1;
+    for (int i = 0; i < noutputs && i < (int)outs.size(); i++) outputs[i] = wrap(outs[i]);
+    return (int)outs.size();
+}
+
+int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs)
+{
+    clear_error();
+    Plan &p = *g->plan;
+    if (p.pending) {
+        set_runtime("FusionGraph already has a pending replay");
+        return -1;
+    }
+    std::vector<TensorP> ins, outs;
+    if (!bind(p, inputs, ninputs, ins)) return -1;
+    if (!execute(p, ins, outs, false)) return -1;
+    if (!p.done && !check_status(pt_event_create(&p.done), "event")) return -1;
+    if (!check_status(pt_event_record(p.done, nullptr), "event record")) return -1;
+    p.pending = true;
+    p.pending_values = outs;
+    for (const TensorP &t : ins) p.pending_values.push_back(t);  // inputs retained until wait()
+    return 0;
+}
+
+int phpt_graph_wait(phpt_graph *g, phpt_tensor **outputs, int noutputs)
+{
+    clear_error();
+    Plan &p = *g->plan;
+    if (!p.pending) {
+        set_runtime("No pending FusionGraph replay");
+        return -1;
+    }
+    if (!check_status(pt_event_synchronize(p.done), "Fusion wait failed")) return -1;
+    p.synchronizations++;
+    int n = (int)p.outputs.size();
+    for (int i = 0; i < noutputs && i < n; i++) outputs[i] = wrap(p.pending_values[i]);
+    p.pending = false;
+    p.pending_values.clear();
+    return n;
+}
+
+int phpt_graph_is_finished(phpt_graph *g)
+{
+    Plan &p = *g->plan;
+    if (!p.pending) return 1;
+    int fin = 0;
+    if (!check_status(pt_event_query(p.done, &fin), "event query")) return -1;
+    return fin;
+}
+
+int phpt_graph_num_outputs(phpt_graph *g) { return (int)g->plan->outputs.size(); }
+
+const char *phpt_graph_source(phpt_graph *g) { return g->plan->source.c_str(); }
+
+const char *phpt_graph_stats(phpt_graph *g)
+{
+    Plan &p = *g->plan;
+    size_t boundaries = 0, intermediates = 0;
+    bool native_present = false;
+    for (Step &st : p.steps) {
+        if (st.native) {
+            boundaries++;
+            native_present = true;
+        }
+    }
+    for (Kernel &k : p.kernels)
+        for (int r : k.roots)
+            if (!p.items[r].output) intermediates++;
+    std::ostringstream os;
+    os << "nodes=" << p.items.size() << ";fusedKernels=" << p.kernels.size() << ";boundaries=" << boundaries
+       << ";executions=" << p.executions << ";executionSteps=" << p.steps.size()
+       << ";intermediateBuffers=" << intermediates << ";cacheHit=" << (p.cache_hit ? 1 : 0)
+       << ";backend=" << (p.use_graph ? "cuda-graph" : "stream")
+       << ";asyncCompatible=1;cudaGraphCompatible=" << (p.graph_compatible ? 1 : 0)
+       << ";graphReplay=" << (p.use_graph && !native_present ? 1 : 0)
+       << ";graphLaunches=" << p.graph_launches << ";bufferReuses=" << p.buffer_reuses
+       << ";pending=" << (p.pending ? 1 : 0) << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)
+       << ";tensorAllocations=" << p.tensor_allocations << ";synchronizations=" << p.synchronizations
+       << ";workspaceBuffers=" << p.cache.size() << ";profiling=" << (p.profiling ? 1 : 0)
+       << ";profiledExecutions=" << p.profiled << ";bindTimeNs=" << p.bind_ns
+       << ";executeTimeNs=" << p.execute_ns << ";collectTimeNs=" << p.collect_ns << ";";
+    t_text = os.str();
+    return t_text.c_str();
+}
+
+const char *phpt_graph_plan(phpt_graph *g)
+{
+    Plan &p = *g->plan;
+    std::ostringstream os;
+    for (Step &st : p.steps) {
+        if (st.native) {
+            static const char *names[] = {"native-matmul", "native-reduction", "native-reduction",
+                                          "native-moments", "native-softmax", "native-layernorm"};
+            os << "native:" << names[p.items[st.item].t->node->native.kind] << ";";
+        } else {
+            Kernel &k = p.kernels[st.kernel];
+            os << "kernel:" << k.name << "(roots=" << k.roots.size() << ",leaves=" << k.leaves.size()
+               << (k.affine ? ",vector" : ",scalar") << ");";
+        }
+    }
+    t_text = os.str();
+    return t_text.c_str();
+}
+
+void phpt_graph_set_profiling(phpt_graph *g, int enabled)
+{
+    Plan &p = *g->plan;
+    p.profiling = enabled != 0;
+    p.profiled = 0;
+    p.bind_ns = p.execute_ns = p.collect_ns = 0;
+}
+
+void phpt_graph_release(phpt_graph *g)
+{
+    if (!g) return;
+    Plan &p = *g->plan;
+    if (p.pending) pt_event_synchronize(p.done);
+    if (p.graph) pt_graph_destroy(p.graph);
+    if (p.done) pt_event_destroy(p.done);
+    delete g->plan;
+    delete g;
+}
+
+const char *phpt_fusion_cache_stats(void)
+{
+    std::lock_guard<std::mutex> lock(g_cache.mu);
+    std::ostringstream os;
+    os << "entries=" << g_cache.modules.size() << ";capacity=" << kCacheEntries << ";hits=" << g_cache.hits
+       << ";misses=" << g_cache.misses << ";evictions=" << g_cache.evictions << ";";
+    t_text = os.str();
+    return t_text.c_str();
+}
+
+void phpt_fusion_clear_cache(void)
+{
+    std::lock_guard<std::mutex> lock(g_cache.mu);
+    g_cache.modules.clear();
+    g_cache.order.clear();
+}
+
+}  // extern "C"

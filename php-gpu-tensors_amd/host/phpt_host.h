@@ -1,0 +1,102 @@
+/*
+ * phpt_host.h — C API of the host runtime (libphptensors_host.so).
+ *
+ * This is the host-side mirror of the reference's CudaArray / Fusion
+ * operator surface (src/cuda_array/cuda_array_ce.c, src/fusion.c), the
+ * layer a PHP extension's Zend glue would call.  It sits above the device
+ * C-ABI of include/pt_hip.h and never touches HIP itself.  Tensors are
+ * opaque reference-counted handles; every call that can fail returns NULL
+ * (or a negative value) and records an error retrievable with
+ * phpt_error_kind() (1 = InvalidArgumentException, 2 = RuntimeException)
+ * and phpt_error_message().
+ */
+#ifndef PHPT_HOST_H
+#define PHPT_HOST_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct phpt_tensor phpt_tensor;
+typedef struct phpt_graph phpt_graph;
+
+#define PHPT_GLOBAL_AXIS (-1000)
+
+int phpt_error_kind(void);
+const char *phpt_error_message(void);
+void phpt_clear_error(void);
+
+/* ---- lifecycle / transfers (tensor_factory.c, tensor_transfer.c) ---- */
+phpt_tensor *phpt_from_host(const void *data, int dtype, const int *shape, int ndims);
+phpt_tensor *phpt_full(const int *shape, int ndims, int dtype, double value, int64_t ivalue, int kind);
+int phpt_to_host(phpt_tensor *t, void *out, size_t bytes);
+phpt_tensor *phpt_retain(phpt_tensor *t);
+void phpt_release(phpt_tensor *t);
+int phpt_dtype(phpt_tensor *t);
+int phpt_ndims(phpt_tensor *t);
+void phpt_shape(phpt_tensor *t, int *shape);
+void phpt_strides(phpt_tensor *t, size_t *strides);
+size_t phpt_size(phpt_tensor *t);
+int phpt_is_lazy(phpt_tensor *t);
+int phpt_dtype_from_name(const char *name);
+const char *phpt_dtype_name(int dtype);
+
+/* ---- views ---- */
+phpt_tensor *phpt_reshape(phpt_tensor *t, const int *shape, int ndims);
+phpt_tensor *phpt_transpose(phpt_tensor *t, const int *perm, int nperm);
+phpt_tensor *phpt_broadcast_to(phpt_tensor *t, const int *shape, int ndims);
+phpt_tensor *phpt_slice(phpt_tensor *t, int axis, int start, int stop, int step);
+phpt_tensor *phpt_select(phpt_tensor *t, int axis, int index);
+
+/* ---- operations (ca_private.c / cuda_array_ce.c) ---- */
+/* scalar kind: 0 = float (value), 1 = int (ivalue), 2 = bool (ivalue) */
+phpt_tensor *phpt_binary(phpt_tensor *a, phpt_tensor *b, int op);
+phpt_tensor *phpt_scalar_op(phpt_tensor *a, double value, int64_t ivalue, int kind, int op, int reverse);
+phpt_tensor *phpt_unary(phpt_tensor *a, int op);
+phpt_tensor *phpt_reduce(phpt_tensor *a, int axis, int op);
+phpt_tensor *phpt_reduce_arg(phpt_tensor *a, int axis, int op);
+phpt_tensor *phpt_variance(phpt_tensor *a, int axis, long correction, int std_dev);
+phpt_tensor *phpt_softmax(phpt_tensor *a, int axis);
+phpt_tensor *phpt_layernorm(phpt_tensor *a, const int *axes, int naxes, double eps,
+                            phpt_tensor *scale, phpt_tensor *bias);
+phpt_tensor *phpt_matmul(phpt_tensor *a, phpt_tensor *b);
+phpt_tensor *phpt_where(phpt_tensor *c, phpt_tensor *x, phpt_tensor *y);
+phpt_tensor *phpt_astype(phpt_tensor *a, int dtype);
+phpt_tensor *phpt_copy(phpt_tensor *a);
+
+/* ---- Fusion (fusion.c, fusion_capture.c, fusion_plan.c, fusion_execute.c) ---- */
+int phpt_fusion_begin(int compiling);
+int phpt_fusion_active(void);
+void phpt_fusion_abort(void);
+phpt_tensor *phpt_fusion_input(phpt_tensor *example, int index);
+/* Ends the scope and builds the plan whose roots are `outputs`.  For a
+ * compile() scope the result is reusable; run() scopes call
+ * phpt_fusion_run_once instead. */
+phpt_graph *phpt_fusion_end(phpt_tensor **outputs, int count, int use_graph);
+/* Ends a run() scope: executes once and replaces every lazy output (and
+ * every recorded value still referenced elsewhere) with its result. */
+int phpt_fusion_run_once(phpt_tensor **outputs, int count);
+int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor **outputs, int noutputs);
+int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs);
+int phpt_graph_wait(phpt_graph *g, phpt_tensor **outputs, int noutputs);
+int phpt_graph_is_finished(phpt_graph *g);
+int phpt_graph_num_outputs(phpt_graph *g);
+const char *phpt_graph_source(phpt_graph *g);
+/* Statistics as "key=value;" pairs (FusionGraph::getStats, fusion.c:723-772). */
+const char *phpt_graph_stats(phpt_graph *g);
+/* Steps as "kind:detail;" entries (FusionGraph::getPlan). */
+const char *phpt_graph_plan(phpt_graph *g);
+void phpt_graph_set_profiling(phpt_graph *g, int enabled);
+void phpt_graph_release(phpt_graph *g);
+/* Module cache counters (Fusion::getCacheStats, fusion_cache.c:50-62). */
+const char *phpt_fusion_cache_stats(void);
+void phpt_fusion_clear_cache(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

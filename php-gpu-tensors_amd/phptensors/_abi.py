@@ -113,6 +113,7 @@ SIGNATURES = {
     "pt_matmul_set_precision": (ctypes.c_int, [ctypes.c_int]),
     "pt_matmul_precision_name": (ctypes.c_char_p, []),
     "pt_matmul_set_tile": (ctypes.c_int, [ctypes.c_int]),
+    "pt_matmul_set_schedule": (ctypes.c_int, [ctypes.c_int]),
     "pt_backend_info_get": (ctypes.c_int, [ctypes.POINTER(PtBackendInfo)]),
     "pt_backend_info_reset": (ctypes.c_int, []),
     "pt_broadcast": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, ctypes.c_size_t,
