@@ -140,6 +140,87 @@ def reduce_family(steps, warmup):
     return fam
 
 
+# ---------------------------------------------------------------- config 3
+def fused_family(steps, warmup, replays=100):
+    """Fusion::compile of tanh(x + y*z), replayed through its HIP graph."""
+    from phptensors import CudaArray, Fusion
+    lib = A.load()
+    rows, n = 16384, 8192
+    x = CudaArray.fromNumpy(synthetic.uniform((rows, n), -2.0, 2.0, seed=3))
+    z = CudaArray.fromNumpy(synthetic.uniform((rows, n), -2.0, 2.0, seed=31))
+    y = CudaArray.fromNumpy(synthetic.uniform((n,), -2.0, 2.0, seed=32))
+    graph = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z], cudaGraph=True)
+    plan = graph.getPlan()
+    bytes_per = 3 * rows * n * 4 + n * 4
+    ev0, ev1 = ctypes.c_void_p(), ctypes.c_void_p()
+    A.check(lib.pt_event_create(ctypes.byref(ev0)), "event")
+    A.check(lib.pt_event_create(ctypes.byref(ev1)), "event")
+
+    def timed(count):
+        # the plan runs on the runtime stream (NULL handle); events go there too
+        A.check(lib.pt_event_record(ev0, None), "record")
+        graph.replay(count, x, y, z)
+        A.check(lib.pt_event_record(ev1, None), "record")
+        A.check(lib.pt_event_synchronize(ev1), "sync")
+        ms = ctypes.c_float()
+        A.check(lib.pt_event_elapsed_ms(ev0, ev1, ctypes.byref(ms)), "elapsed")
+        return ms.value / count
+
+    timed(max(1, warmup) * 10)
+    samples = sorted(timed(replays) for _ in range(max(1, steps // 5)))
+    ms = samples[len(samples) // 2]
+    # FusionGraph::run as the reference calls it: bind, replay, synchronize per call
+    t0 = time.perf_counter()
+    for _ in range(10):
+        graph.run(x, y, z)
+    run_ms = (time.perf_counter() - t0) / 10 * 1e3
+    stats = graph.getStats()
+    lib.pt_event_destroy(ev0)
+    lib.pt_event_destroy(ev1)
+    gbs = bytes_per / (ms * 1e-3) / 1e9
+    log(f"fused tanh(x+y*z): {ms * 1e3:.1f} us/replay  {gbs:.0f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM;"
+        f" run() incl. bind+sync {run_ms * 1e3:.1f} us")
+    res = {"ms": ms, "bytes": bytes_per, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "kernel": "fk0_v",
+           "run_ms_with_sync": run_ms, "replays_per_sample": replays}
+    return {"workload": "config3: Fusion tanh(x + y*z), x,z [16384,8192] U(-2,2) seeds 3/31, "
+                        "y [8192] seed 32; compiled once, replayed 100x via hipGraph",
+            "ms_per_step": ms * replays, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS,
+            "ops": {"tanh_x_plus_y_z": res}, "plan": plan,
+            "stats": {k: stats[k] for k in ("fusedKernels", "graphLaunches", "cudaGraphCompatible")}}
+
+
+def fused_cpu_baseline(sample_rows=512):
+    """Oracle tanh(x + y*z) (per-op rounding, libm tanhf, 1 thread) on a row sample."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    n = 8192
+    x = synthetic.uniform((sample_rows, n), -2.0, 2.0, seed=3)
+    z = synthetic.uniform((sample_rows, n), -2.0, 2.0, seed=31)
+    y = synthetic.uniform((n,), -2.0, 2.0, seed=32)
+    t0 = time.perf_counter()
+    m = O.binary(y, O.F32, z, O.F32, "mul", O.F32)
+    s = O.binary(x, O.F32, m, O.F32, "add", O.F32)
+    O.unary(s, O.F32, "tanh")
+    dt = time.perf_counter() - t0
+    b = 3 * x.nbytes + y.nbytes
+    return {"value": b / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{sample_rows} of 16384 rows of config 3 on one host core; {dt:.2f} s"}
+
+
+def gemm_cpu_baseline(sample_rows=128):
+    """Oracle matmul (sequential fmaf per output, 1 thread) on a row sample of one batch."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    k = n = 2048
+    a = synthetic.normal((32, 2048, k), 0.0, 0.02, seed=4)[0, :sample_rows]
+    b = synthetic.normal((32, k, n), 0.0, 0.02, seed=5)[0]
+    t0 = time.perf_counter()
+    O.matmul(a, b, O.F32)
+    dt = time.perf_counter() - t0
+    return {"value": 2.0 * sample_rows * k * n / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"fp32, rows 0..{sample_rows - 1} of batch 0 of config 4 on one host core; {dt:.2f} s"}
+
+
 # ---------------------------------------------------------------- config 4
 def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
     lib = A.load()
@@ -210,6 +291,16 @@ def reduce_cpu_baseline():
                       f"{dt:.2f} s", "seconds": dt}
 
 
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -242,6 +333,8 @@ def main():
     only = set(args.only.split(","))
     if "reduce" in only:
         fams["reduce"] = reduce_family(args.steps, args.warmup)
+    if "fused" in only:
+        fams["fused"] = fused_family(args.steps, args.warmup)
     if "gemm" in only:
         fams["gemm"] = gemm_family(args.steps, args.warmup)
     wall = time.perf_counter() - t_wall
@@ -268,8 +361,12 @@ def main():
     cpu = None
     if not args.no_cpu and "reduce" in fams:
         cpu = reduce_cpu_baseline()
-        cpu["cpu_model"] = platform.processor() or platform.machine()
+        cpu["cpu_model"] = _cpu_model()
         cpu["nproc"] = os.cpu_count()
+        if "fused" in fams:
+            fams["fused"]["cpu_baseline"] = fused_cpu_baseline()
+        if "gemm" in fams:
+            fams["gemm"]["cpu_baseline"] = gemm_cpu_baseline()
     ms_step = sum(f["ms_per_step"] for f in fams.values())
     line = {
         "metric": "GEMM TFLOP/s + reduce/fused-eltwise HBM GB/s, % of MI355X peak, 1 GPU",

@@ -472,8 +472,8 @@ static void gather(const Plan &p, Kernel &k, int id, const CoordMap &cm, bool &a
 // ------------------------------------------------------ code generation
 static void emit_prelude(std::ostringstream &os)
 {
-    os << "#include <hip/hip_runtime.h>\n"
-          "__device__ __forceinline__ float pt_b2f(unsigned short b){return __uint_as_float(((unsigned)b)<<16);}\n"
+    // hipRTC provides the HIP device builtins and vector types itself
+    os << "__device__ __forceinline__ float pt_b2f(unsigned short b){return __uint_as_float(((unsigned)b)<<16);}\n"
           "__device__ __forceinline__ unsigned short pt_f2b(float f){unsigned u=__float_as_uint(f);"
           "if((u&0x7f800000u)==0x7f800000u&&(u&0x7fffffu))return (unsigned short)((u>>16)|0x40u);"
           "return (unsigned short)((u+0x7fffu+((u>>16)&1u))>>16);}\n"
@@ -1189,6 +1189,31 @@ int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor
     if (!execute(p, ins, outs, true)) return -1;
     for (int i = 0; i < noutputs && i < (int)outs.size(); i++) outputs[i] = wrap(outs[i]);
     return (int)outs.size();
+}
+
+int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count)
+{
+    clear_error();
+    Plan &p = *g->plan;
+    if (p.pending) {
+        set_runtime("FusionGraph has a pending asynchronous replay; wait() first");
+        return -1;
+    }
+    if (count < 1) {
+        set_invalid("Replay count must be positive");
+        return -1;
+    }
+    std::vector<TensorP> ins, outs;
+    if (!bind(p, inputs, ninputs, ins)) return -1;
+    // outputs are dropped between replays, so every replay reuses the same
+    // buffers and the captured graph; one synchronization at the end
+    for (int i = 0; i < count; i++) {
+        if (!execute(p, ins, outs, false)) return -1;
+        outs.clear();
+    }
+    if (!check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed")) return -1;
+    p.synchronizations++;
+    return 0;
 }
 
 int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs)

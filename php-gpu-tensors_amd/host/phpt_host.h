@@ -80,6 +80,11 @@ phpt_graph *phpt_fusion_end(phpt_tensor **outputs, int count, int use_graph);
  * every recorded value still referenced elsewhere) with its result. */
 int phpt_fusion_run_once(phpt_tensor **outputs, int count);
 int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor **outputs, int noutputs);
+/* Replays the plan `count` times back to back on the runtime stream and
+ * synchronizes once (outputs are discarded).  No counterpart in the
+ * reference, whose run() synchronizes per replay (fusion.c:599-641); it
+ * exists to time replay throughput. */
+int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count);
 int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs);
 int phpt_graph_wait(phpt_graph *g, phpt_tensor **outputs, int noutputs);
 int phpt_graph_is_finished(phpt_graph *g);

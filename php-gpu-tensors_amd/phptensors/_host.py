@@ -54,6 +54,7 @@ SIGNATURES = {
     "phpt_fusion_end": (G, [ctypes.POINTER(T), ctypes.c_int, ctypes.c_int]),
     "phpt_fusion_run_once": (ctypes.c_int, [ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_run": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.POINTER(T), ctypes.c_int]),
+    "phpt_graph_replay": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.c_int]),
     "phpt_graph_run_async": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_wait": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_is_finished": (ctypes.c_int, [G]),

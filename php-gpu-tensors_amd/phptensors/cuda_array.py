@@ -1,0 +1,449 @@
+"""CudaArray: the reference's PhpTensors\\CudaArray surface for the hot path,
+over the host runtime (host/phpt_host.h) and the gfx950 C-ABI.
+
+Method names, argument meaning and exception types follow
+stubs/cuda.stub.php (CudaArray, :410-620 of that file) so that a test written
+against the PHP class reads the same here.  Every operation runs on the GPU;
+when the HIP libraries are not built, the first call raises RuntimeException.
+"""
+import ctypes
+import numbers
+
+import numpy as np
+
+from . import _abi, _host
+from ._abi import InvalidArgumentException, RuntimeException  # noqa: F401
+
+GLOBAL_AXIS = -1000
+
+# include/pt_hip.h dtype codes and the names the reference prints
+DTYPES = {
+    "float32": 0, "float64": 1, "int8": 2, "int16": 3, "int32": 4, "int64": 5,
+    "uint8": 6, "uint16": 7, "uint32": 8, "uint64": 9, "bool": 10,
+    "float16": 11, "bfloat16": 12,
+}
+DTYPE_NAMES = {v: k for k, v in DTYPES.items()}
+NUMPY_OF = {
+    0: np.float32, 1: np.float64, 2: np.int8, 3: np.int16, 4: np.int32, 5: np.int64,
+    6: np.uint8, 7: np.uint16, 8: np.uint32, 9: np.uint64, 10: np.bool_,
+    11: np.float16, 12: np.uint16,   # bfloat16 travels as its 16-bit pattern
+}
+CODE_OF_NUMPY = {np.dtype(v): k for k, v in NUMPY_OF.items() if k not in (12,)}
+# host storage of element bit patterns (both 16-bit float types as uint16)
+BITS_OF = dict(NUMPY_OF)
+BITS_OF[11] = np.uint16
+
+# include/pt_hip.h operation codes (operation_type_t of the reference)
+OP = dict(ADD=0, SUB=1, MUL=2, DIV=3, POW=4, EXP=5, EXPM1=6, SQRT=7, LOG=8, LOG1P=9,
+          EXP2=10, LOG2=11, LOG10=12, ASIN=13, ACOS=14, ATAN=15, SINH=16, COSH=17,
+          TANH=18, SIN=19, COS=20, TAN=21, ABS=22, NEG=23, CEIL=26, FLOOR=27, ROUND=28,
+          GT=29, LT=30, EQ=31, NE=32, GE=33, LE=34, SUM=35, MEAN=36, MAX=37, MIN=38,
+          PROD=39, ARG_MAX=42, ARG_MIN=43, MAXIMUM=54, MINIMUM=55)
+
+
+def dtype_code(dtype):
+    if dtype is None:
+        return DTYPES["float32"]
+    if isinstance(dtype, int):
+        return dtype
+    code = _host.load().phpt_dtype_from_name(str(dtype).encode())
+    if code < 0:
+        raise InvalidArgumentException(f"Unknown dtype '{dtype}'")
+    return code
+
+
+def bf16_bits_to_f32(bits):
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(x):
+    """Round-to-nearest-even float32 -> bfloat16 bit pattern (data_types.c:96-131)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    return np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+
+
+def _scalar_args(value):
+    if isinstance(value, (bool, np.bool_)):
+        return 0.0, int(bool(value)), 2
+    if isinstance(value, numbers.Integral):
+        return 0.0, int(value), 1
+    if isinstance(value, numbers.Real):
+        return float(value), 0, 0
+    raise InvalidArgumentException(f"Unsupported scalar operand of type {type(value).__name__}")
+
+
+def _ints(seq):
+    seq = [int(v) for v in seq]
+    return (ctypes.c_int * max(1, len(seq)))(*seq), len(seq)
+
+
+class CudaArray:
+    """GPU tensor handle (src/tensor.h tensor_t behind a CudaArray object)."""
+
+    __slots__ = ("_h", "__weakref__")
+
+    def __init__(self, data=None, dtype="float32"):
+        self._h = None
+        if data is None:
+            return
+        arr = np.asarray(data)
+        h = _from_numpy(arr, dtype_code(dtype))
+        self._h = h
+
+    @classmethod
+    def _wrap(cls, handle, what=""):
+        _host.check_handle(handle, what)
+        obj = cls.__new__(cls)
+        obj._h = handle
+        return obj
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h and _host._lib is not None:
+            _host._lib.phpt_release(h)
+            self._h = None
+
+    # ------------------------------------------------------------ factories
+    @classmethod
+    def fromNumpy(cls, arr, dtype=None):
+        """Upload a host array (HostArray::toGpu -> tensor_factory.c:301-326).
+        float16 / bfloat16 input is given either as uint16 bit patterns or as
+        values (rounded to nearest even)."""
+        arr = np.asarray(arr)
+        code = dtype_code(dtype) if dtype is not None else CODE_OF_NUMPY.get(arr.dtype)
+        if code is None:
+            raise InvalidArgumentException(f"Unsupported host dtype {arr.dtype}")
+        return cls._wrap(_from_numpy(arr, code), "fromNumpy")
+
+    @classmethod
+    def fromFlatArray(cls, values, shape, dtype="float32"):
+        return cls.fromNumpy(np.asarray(values).reshape(shape), dtype)
+
+    @classmethod
+    def fromBuffer(cls, data, shape, dtype="float32"):
+        """Raw little-endian element bytes (cuda_array_ce.c:151-187)."""
+        code = dtype_code(dtype)
+        arr = np.frombuffer(bytes(data), dtype=NUMPY_OF[code])
+        n = int(np.prod(shape)) if len(shape) else 1
+        if arr.size != n:
+            raise InvalidArgumentException(
+                f"Buffer holds {arr.size} elements, shape needs {n}")
+        return cls._wrap(_from_bits(arr.reshape(shape), code), "fromBuffer")
+
+    @classmethod
+    def full(cls, shape, value, dtype="float32"):
+        v, iv, kind = _scalar_args(value)
+        sh, n = _ints(shape)
+        return cls._wrap(_host.load().phpt_full(sh, n, dtype_code(dtype), v, iv, kind), "full")
+
+    @classmethod
+    def zeros(cls, shape, dtype="float32"):
+        return cls.full(shape, 0, dtype)
+
+    @classmethod
+    def ones(cls, shape, dtype="float32"):
+        return cls.full(shape, 1, dtype)
+
+    @classmethod
+    def where(cls, condition, x, y):
+        return cls._wrap(_host.load().phpt_where(condition._h, x._h, y._h), "where")
+
+    # ------------------------------------------------------------ metadata
+    def getShape(self):
+        lib = _host.load()
+        nd = lib.phpt_ndims(self._h)
+        buf = (ctypes.c_int * max(1, nd))()
+        lib.phpt_shape(self._h, buf)
+        return [buf[i] for i in range(nd)]
+
+    @property
+    def shape(self):
+        return tuple(self.getShape())
+
+    def getStrides(self):
+        lib = _host.load()
+        nd = lib.phpt_ndims(self._h)
+        buf = (ctypes.c_size_t * max(1, nd))()
+        lib.phpt_strides(self._h, buf)
+        return [buf[i] for i in range(nd)]
+
+    def getNdims(self):
+        return _host.load().phpt_ndims(self._h)
+
+    def getSize(self):
+        return int(_host.load().phpt_size(self._h))
+
+    def count(self):
+        return self.getSize()
+
+    def getDtype(self):
+        return DTYPE_NAMES[_host.load().phpt_dtype(self._h)]
+
+    dtype = getDtype
+
+    def dtypeCode(self):
+        return _host.load().phpt_dtype(self._h)
+
+    def isLazy(self):
+        return bool(_host.load().phpt_is_lazy(self._h))
+
+    # ------------------------------------------------------------ transfers
+    def toBits(self):
+        """Element bit patterns in a numpy array (float16 / bfloat16 as uint16)."""
+        code = self.dtypeCode()
+        out = np.empty(self.shape, dtype=BITS_OF[code])
+        if _host.load().phpt_to_host(self._h, out.ctypes.data_as(ctypes.c_void_p), out.nbytes) != 0:
+            _host.raise_error("toHost")
+        return out
+
+    def toNumpy(self):
+        """Values in numpy (bfloat16 widened to float32)."""
+        bits = self.toBits()
+        code = self.dtypeCode()
+        if code == DTYPES["bfloat16"]:
+            return bf16_bits_to_f32(bits)
+        if code == DTYPES["float16"]:
+            return bits.view(np.float16)
+        return bits
+
+    def toArray(self):
+        return self.toNumpy().tolist()
+
+    def toBuffer(self):
+        """Raw element bytes, row-major (cuda_array_ce.c:2943-2951)."""
+        return self.toBits().tobytes()
+
+    def item(self):
+        if self.getSize() != 1:
+            raise InvalidArgumentException("item() requires a tensor with exactly one element")
+        return self.toNumpy().reshape(-1)[0].item()
+
+    # ------------------------------------------------------------ elementwise
+    def _binary(self, other, op, reverse=False):
+        lib = _host.load()
+        if isinstance(other, CudaArray):
+            a, b = (other, self) if reverse else (self, other)
+            return CudaArray._wrap(lib.phpt_binary(a._h, b._h, op))
+        v, iv, kind = _scalar_args(other)
+        return CudaArray._wrap(lib.phpt_scalar_op(self._h, v, iv, kind, op, 1 if reverse else 0))
+
+    def add(self, other):
+        return self._binary(other, OP["ADD"])
+
+    def subtract(self, other):
+        return self._binary(other, OP["SUB"])
+
+    def multiply(self, other):
+        return self._binary(other, OP["MUL"])
+
+    def divide(self, other):
+        return self._binary(other, OP["DIV"])
+
+    def power(self, other):
+        return self._binary(other, OP["POW"])
+
+    def maximum(self, other):
+        return self._binary(other, OP["MAXIMUM"])
+
+    def minimum(self, other):
+        return self._binary(other, OP["MINIMUM"])
+
+    def gt(self, other):
+        return self._binary(other, OP["GT"])
+
+    def lt(self, other):
+        return self._binary(other, OP["LT"])
+
+    def eq(self, other):
+        return self._binary(other, OP["EQ"])
+
+    def ne(self, other):
+        return self._binary(other, OP["NE"])
+
+    def ge(self, other):
+        return self._binary(other, OP["GE"])
+
+    def le(self, other):
+        return self._binary(other, OP["LE"])
+
+    def clamp(self, min=None, max=None):
+        out = self
+        if min is not None:
+            out = out.maximum(min)
+        if max is not None:
+            out = out.minimum(max)
+        return out if out is not self else self.copy()
+
+    __add__ = add
+    __sub__ = subtract
+    __mul__ = multiply
+    __truediv__ = divide
+    __pow__ = power
+
+    def __radd__(self, other):
+        return self._binary(other, OP["ADD"], reverse=True)
+
+    def __rsub__(self, other):
+        return self._binary(other, OP["SUB"], reverse=True)
+
+    def __rmul__(self, other):
+        return self._binary(other, OP["MUL"], reverse=True)
+
+    def __rtruediv__(self, other):
+        return self._binary(other, OP["DIV"], reverse=True)
+
+    def __rpow__(self, other):
+        return self._binary(other, OP["POW"], reverse=True)
+
+    def __neg__(self):
+        return self.neg()
+
+    def __matmul__(self, other):
+        return self.matmul(other)
+
+    def _unary(self, op):
+        return CudaArray._wrap(_host.load().phpt_unary(self._h, op))
+
+    def sqrt(self): return self._unary(OP["SQRT"])
+    def exp(self): return self._unary(OP["EXP"])
+    def expm1(self): return self._unary(OP["EXPM1"])
+    def exp2(self): return self._unary(OP["EXP2"])
+    def log(self): return self._unary(OP["LOG"])
+    def log1p(self): return self._unary(OP["LOG1P"])
+    def log2(self): return self._unary(OP["LOG2"])
+    def log10(self): return self._unary(OP["LOG10"])
+    def sin(self): return self._unary(OP["SIN"])
+    def cos(self): return self._unary(OP["COS"])
+    def tan(self): return self._unary(OP["TAN"])
+    def asin(self): return self._unary(OP["ASIN"])
+    def acos(self): return self._unary(OP["ACOS"])
+    def atan(self): return self._unary(OP["ATAN"])
+    def sinh(self): return self._unary(OP["SINH"])
+    def cosh(self): return self._unary(OP["COSH"])
+    def tanh(self): return self._unary(OP["TANH"])
+    def abs(self): return self._unary(OP["ABS"])
+    def neg(self): return self._unary(OP["NEG"])
+    def floor(self): return self._unary(OP["FLOOR"])
+    def ceil(self): return self._unary(OP["CEIL"])
+    def round(self): return self._unary(OP["ROUND"])
+
+    def astype(self, dtype):
+        return CudaArray._wrap(_host.load().phpt_astype(self._h, dtype_code(dtype)))
+
+    def copy(self):
+        return CudaArray._wrap(_host.load().phpt_copy(self._h))
+
+    # ------------------------------------------------------------ reductions
+    @staticmethod
+    def _axis(axis):
+        return GLOBAL_AXIS if axis is None else int(axis)
+
+    def _reduce(self, axis, op):
+        return CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), op))
+
+    def sum(self, axis=None): return self._reduce(axis, OP["SUM"])
+    def mean(self, axis=None): return self._reduce(axis, OP["MEAN"])
+    def max(self, axis=None): return self._reduce(axis, OP["MAX"])
+    def min(self, axis=None): return self._reduce(axis, OP["MIN"])
+    def prod(self, axis=None): return self._reduce(axis, OP["PROD"])
+
+    def argMax(self, axis=None):
+        return CudaArray._wrap(_host.load().phpt_reduce_arg(self._h, self._axis(axis), OP["ARG_MAX"]))
+
+    def argMin(self, axis=None):
+        return CudaArray._wrap(_host.load().phpt_reduce_arg(self._h, self._axis(axis), OP["ARG_MIN"]))
+
+    def var(self, axis=None, correction=0):
+        return CudaArray._wrap(_host.load().phpt_variance(self._h, self._axis(axis), int(correction), 0))
+
+    def std(self, axis=None, correction=0):
+        return CudaArray._wrap(_host.load().phpt_variance(self._h, self._axis(axis), int(correction), 1))
+
+    def softmax(self, axis=-1):
+        return CudaArray._wrap(_host.load().phpt_softmax(self._h, int(axis)))
+
+    def layerNorm(self, axes, epsilon=1e-5, scale=None, bias=None):
+        ax, n = _ints(axes)
+        return CudaArray._wrap(_host.load().phpt_layernorm(
+            self._h, ax, n, float(epsilon), scale._h if scale is not None else None,
+            bias._h if bias is not None else None))
+
+    def matmul(self, other):
+        if not isinstance(other, CudaArray):
+            raise InvalidArgumentException("matmul() expects a CudaArray operand")
+        return CudaArray._wrap(_host.load().phpt_matmul(self._h, other._h))
+
+    # ------------------------------------------------------------ views
+    def reshape(self, shape):
+        sh, n = _ints(shape)
+        return CudaArray._wrap(_host.load().phpt_reshape(self._h, sh, n))
+
+    def flatten(self):
+        return self.reshape([-1])
+
+    def transpose(self, axis=None):
+        nd = self.getNdims()
+        perm = list(range(nd))[::-1] if axis is None else list(axis)
+        p, n = _ints(perm)
+        return CudaArray._wrap(_host.load().phpt_transpose(self._h, p, n))
+
+    @property
+    def T(self):
+        return self.transpose()
+
+    def swapaxes(self, axis1, axis2):
+        nd = self.getNdims()
+        perm = list(range(nd))
+        a1, a2 = axis1 % nd if nd else 0, axis2 % nd if nd else 0
+        perm[a1], perm[a2] = perm[a2], perm[a1]
+        return self.transpose(perm)
+
+    def broadcastTo(self, shape):
+        sh, n = _ints(shape)
+        return CudaArray._wrap(_host.load().phpt_broadcast_to(self._h, sh, n))
+
+    def slice(self, axis, start, stop, step=1):
+        return CudaArray._wrap(_host.load().phpt_slice(self._h, int(axis), int(start), int(stop), int(step)))
+
+    def select(self, axis, index):
+        return CudaArray._wrap(_host.load().phpt_select(self._h, int(axis), int(index)))
+
+    def unsqueeze(self, axis):
+        shape = self.getShape()
+        axis = axis + len(shape) + 1 if axis < 0 else axis
+        shape.insert(axis, 1)
+        return self.reshape(shape)
+
+    def squeeze(self, axis=None):
+        shape = self.getShape()
+        if axis is None:
+            new = [s for s in shape if s != 1]
+        else:
+            axis = axis % len(shape)
+            if shape[axis] != 1:
+                raise InvalidArgumentException("Cannot squeeze an axis whose size is not 1")
+            new = shape[:axis] + shape[axis + 1:]
+        return self.reshape(new)
+
+    def __repr__(self):
+        return f"CudaArray(shape={self.getShape()}, dtype={self.getDtype()})"
+
+
+def _from_bits(arr, code):
+    arr = np.ascontiguousarray(arr)
+    sh, n = _ints(arr.shape)
+    return _host.load().phpt_from_host(arr.ctypes.data_as(ctypes.c_void_p), code, sh, n)
+
+
+def _from_numpy(arr, code):
+    arr = np.asarray(arr)
+    if code in (DTYPES["bfloat16"], DTYPES["float16"]) and arr.dtype == np.uint16:
+        h = _from_bits(arr, code)          # 16-bit patterns as given
+    elif code == DTYPES["bfloat16"]:
+        h = _from_bits(f32_to_bf16_bits(arr.astype(np.float32)), code)
+    else:
+        h = _from_bits(arr.astype(NUMPY_OF[code], copy=False), code)
+    return _host.check_handle(h, "upload")

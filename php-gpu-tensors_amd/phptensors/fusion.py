@@ -1,0 +1,182 @@
+"""Fusion, FusionGraph and FusionExecution (stubs/cuda.stub.php:55-93).
+
+Fusion.run(callback) records the callback's CudaArray operations into a DAG
+and executes the fused plan once (src/fusion.c:250-310); Fusion.compile
+records once against example inputs and returns a FusionGraph that replays
+the plan, optionally from a captured HIP graph (src/fusion.c:312-418,
+599-692).  All recording, planning, code generation (hipRTC for gfx950) and
+execution happen in the host runtime; this module only carries handles and
+the callback's result structure.
+"""
+import ctypes
+
+from . import _host
+from .cuda_array import CudaArray
+from ._abi import InvalidArgumentException, RuntimeException  # noqa: F401
+
+
+def _flatten(result):
+    """Tensors of a callback result, in order, and a rebuild function."""
+    if isinstance(result, CudaArray):
+        return [result], lambda ts: ts[0]
+    if isinstance(result, (list, tuple)):
+        kind = type(result)
+        if not all(isinstance(v, CudaArray) for v in result):
+            raise InvalidArgumentException("Fusion outputs must be CudaArray values")
+        return list(result), lambda ts: kind(ts)
+    if isinstance(result, dict):
+        keys = list(result)
+        if not all(isinstance(result[k], CudaArray) for k in keys):
+            raise InvalidArgumentException("Fusion outputs must be CudaArray values")
+        return [result[k] for k in keys], lambda ts: dict(zip(keys, ts))
+    raise InvalidArgumentException("Fusion callbacks must return a CudaArray or an array of CudaArray")
+
+
+def _handles(tensors):
+    arr = (ctypes.c_void_p * max(1, len(tensors)))()
+    for i, t in enumerate(tensors):
+        arr[i] = t._h
+    return arr
+
+
+class Fusion:
+    """Scoped elementwise fusion; eager operators remain the default."""
+
+    @staticmethod
+    def run(callback, enabled=True):
+        if not enabled:
+            return callback()
+        lib = _host.load()
+        if lib.phpt_fusion_begin(0) != 0:
+            _host.raise_error("Fusion::run")
+        try:
+            result = callback()
+        except BaseException:
+            lib.phpt_fusion_abort()
+            raise
+        try:
+            outs, _ = _flatten(result) if result is not None else ([], None)
+        except BaseException:
+            lib.phpt_fusion_abort()
+            raise
+        if lib.phpt_fusion_run_once(_handles(outs), len(outs)) != 0:
+            _host.raise_error("Fusion::run")
+        return result
+
+    @staticmethod
+    def compile(callback, inputs, cudaGraph=False):
+        lib = _host.load()
+        inputs = list(inputs)
+        for t in inputs:
+            if not isinstance(t, CudaArray):
+                raise InvalidArgumentException("Fusion::compile inputs must be CudaArray values")
+        if lib.phpt_fusion_begin(1) != 0:
+            _host.raise_error("Fusion::compile")
+        try:
+            placeholders = [CudaArray._wrap(lib.phpt_fusion_input(t._h, i)) for i, t in enumerate(inputs)]
+            result = callback(*placeholders)
+            outs, rebuild = _flatten(result)
+        except BaseException:
+            lib.phpt_fusion_abort()
+            raise
+        g = lib.phpt_fusion_end(_handles(outs), len(outs), 1 if cudaGraph else 0)
+        if not g:
+            _host.raise_error("Fusion::compile")
+        return FusionGraph(g, rebuild, len(inputs))
+
+    @staticmethod
+    def getCacheStats():
+        return _host.parse_kv(_host.load().phpt_fusion_cache_stats())
+
+    @staticmethod
+    def clearCache():
+        _host.load().phpt_fusion_clear_cache()
+
+
+class FusionGraph:
+    """Plan specialised for the example inputs' shapes, dtypes and strides."""
+
+    def __init__(self, handle, rebuild, ninputs):
+        self._g = handle
+        self._rebuild = rebuild
+        self._ninputs = ninputs
+
+    def __del__(self):
+        g = getattr(self, "_g", None)
+        if g and _host._lib is not None:
+            _host._lib.phpt_graph_release(g)
+            self._g = None
+
+    def _outputs(self, count):
+        return (ctypes.c_void_p * max(1, count))()
+
+    def run(self, *inputs):
+        lib = _host.load()
+        n = lib.phpt_graph_num_outputs(self._g)
+        outs = self._outputs(n)
+        if lib.phpt_graph_run(self._g, _handles(inputs), len(inputs), outs, n) < 0:
+            _host.raise_error("FusionGraph::run")
+        return self._rebuild([CudaArray._wrap(outs[i]) for i in range(n)])
+
+    def replay(self, count, *inputs):
+        """Replay `count` times back to back and synchronize once, discarding
+        the outputs (throughput measurement; not part of the reference API)."""
+        if _host.load().phpt_graph_replay(self._g, _handles(inputs), len(inputs), int(count)) != 0:
+            _host.raise_error("FusionGraph::replay")
+
+    def runAsync(self, *inputs):
+        lib = _host.load()
+        if lib.phpt_graph_run_async(self._g, _handles(inputs), len(inputs)) != 0:
+            _host.raise_error("FusionGraph::runAsync")
+        return FusionExecution(self)
+
+    def getStats(self):
+        return _host.parse_kv(_host.load().phpt_graph_stats(self._g))
+
+    def getSource(self):
+        return _host.load().phpt_graph_source(self._g).decode()
+
+    def getPlan(self):
+        steps = []
+        for part in _host.load().phpt_graph_plan(self._g).decode().split(";"):
+            if part:
+                kind, _, detail = part.partition(":")
+                steps.append({"kind": kind, "detail": detail})
+        return steps
+
+    def setProfiling(self, enabled):
+        _host.load().phpt_graph_set_profiling(self._g, 1 if enabled else 0)
+
+
+class FusionExecution:
+    """Pending replay; wait() synchronises and returns the outputs."""
+
+    def __init__(self, graph):
+        self._graph = graph
+        self._result = None
+
+    def wait(self):
+        if self._result is None:
+            lib = _host.load()
+            g = self._graph._g
+            n = lib.phpt_graph_num_outputs(g)
+            outs = self._graph._outputs(n)
+            if lib.phpt_graph_wait(g, outs, n) < 0:
+                _host.raise_error("FusionExecution::wait")
+            self._result = self._graph._rebuild([CudaArray._wrap(outs[i]) for i in range(n)])
+        return self._result
+
+    def isFinished(self):
+        if self._result is not None:
+            return True
+        rc = _host.load().phpt_graph_is_finished(self._graph._g)
+        if rc < 0:
+            _host.raise_error("FusionExecution::isFinished")
+        return rc == 1
+
+    def __del__(self):
+        try:
+            if self._result is None and _host._lib is not None:
+                self.wait()
+        except Exception:
+            pass

@@ -25,14 +25,21 @@ NAMES = {
     "int64": I64, "uint8": U8, "uint16": U16, "uint32": U32, "uint64": U64,
     "bool": BOOL, "float16": F16, "bfloat16": BF16,
 }
-OP = {
+class _OpTable(dict):
+    """Operation codes of include/pt_hip.h; names are case-insensitive."""
+
+    def __getitem__(self, key):
+        return dict.__getitem__(self, key.lower())
+
+
+OP = _OpTable({
     "add": 0, "sub": 1, "mul": 2, "div": 3, "exp": 5, "expm1": 6, "sqrt": 7,
     "log": 8, "log1p": 9, "exp2": 10, "log2": 11, "log10": 12, "asin": 13,
     "acos": 14, "atan": 15, "sinh": 16, "cosh": 17, "tanh": 18, "sin": 19,
     "cos": 20, "tan": 21, "abs": 22, "neg": 23, "ceil": 26, "floor": 27,
     "round": 28, "sum": 35, "mean": 36, "max": 37, "min": 38,
-    "argmax": 42, "argmin": 43,
-}
+    "argmax": 42, "argmin": 43, "arg_max": 42, "arg_min": 43,
+})
 
 _lib = None
 

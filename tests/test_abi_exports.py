@@ -33,3 +33,24 @@ def test_status_strings_without_device():
     n = ctypes.c_int(-1)
     assert lib.pt_device_count(ctypes.byref(n)) == 0
     assert n.value >= 0
+
+
+def test_host_runtime_exports_every_declared_symbol():
+    from phptensors import _host
+    header = os.path.join(ROOT, "php-gpu-tensors_amd", "host", "phpt_host.h")
+    text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+    names = sorted(set(re.findall(r"\b(phpt_[a-z0-9_]+)\s*\(", text)))
+    assert len(names) > 40
+    lib = ctypes.CDLL(_host.HOST_LIB)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    assert sorted(_host.SIGNATURES) == names
+
+
+def test_host_runtime_dtype_names_without_device():
+    from phptensors import _host
+    lib = _host.load()
+    assert lib.phpt_dtype_from_name(b"bfloat16") == 12
+    assert lib.phpt_dtype_from_name(b"float32") == 0
+    assert lib.phpt_dtype_from_name(b"nope") == -1
+    assert lib.phpt_dtype_name(11) == b"float16"

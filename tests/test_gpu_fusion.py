@@ -1,0 +1,233 @@
+"""GPU parity of Fusion / FusionGraph / FusionExecution (hipRTC for gfx950,
+HIP graph replay) against the reference's fusion_*.phpt vectors, against the
+eager CudaArray kernels (bitwise: fusion must not contract a+b*c or change
+per-node rounding, fusion_precision.phpt:15-16) and against the CPU oracle."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from phptensors import CudaArray, Fusion, InvalidArgumentException
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_expectations.json")))
+FUSION = {v["id"]: v for v in GOLDEN["fusion"]}
+
+
+def arr(spec):
+    if isinstance(spec, dict):
+        a = np.asarray(spec["data"], dtype=spec.get("dtype", "float32")).reshape(spec["shape"])
+        t = CudaArray.fromNumpy(a, spec.get("dtype", "float32"))
+        return t.transpose() if spec.get("transpose") else t
+    return CudaArray.fromNumpy(np.asarray(spec, np.float32))
+
+
+def bits(t):
+    return t.toBits().view(np.uint8)
+
+
+# ----------------------------------------------------------- golden vectors
+def test_fusion_graph_abc_and_rebinding():
+    g1 = FUSION["fusion_graph_abc"]
+    ins = [arr(g1["inputs"][k]) for k in "abc"]
+    graph = Fusion.compile(lambda a, b, c: a + b * c, ins)
+    out = graph.run(*ins)
+    np.testing.assert_array_equal(out.toNumpy(), g1["expected"])
+    assert graph.getStats()["fusedKernels"] == g1["fused_kernels"]
+    g2 = FUSION["fusion_graph_rebound"]
+    out2 = graph.run(*[arr(g2["inputs"][k]) for k in "abc"])
+    np.testing.assert_array_equal(out2.toNumpy(), g2["expected"])
+    assert graph.getStats()["executions"] == 2
+    assert "extern \"C\" __global__" in graph.getSource()
+
+
+def test_fusion_run_abc():
+    g = FUSION["fusion_run_abc"]
+    a, b, c = (arr(g["inputs"][k]) for k in "abc")
+    out = Fusion.run(lambda: a + b * c)
+    assert not out.isLazy()
+    np.testing.assert_array_equal(out.toNumpy(), g["expected"])
+
+
+def test_fusion_broadcast_cast():
+    g = FUSION["fusion_broadcast_cast"]
+    a, b, c = (arr(g["inputs"][k]) for k in "abc")
+    graph = Fusion.compile(lambda x, y, z: x + y * z, [a, b, c])
+    out = graph.run(a, b, c)
+    assert out.getDtype() == g["expected_dtype"] and out.getShape() == g["expected_shape"]
+    np.testing.assert_array_equal(out.toNumpy().reshape(-1), g["expected"])
+
+
+def test_fusion_transposed_view():
+    g = FUSION["fusion_transposed_view"]
+    v = arr(g["inputs"]["v"])
+    graph = Fusion.compile(lambda x: 100 - x * 2, [v])
+    out = graph.run(v)
+    assert out.getShape() == g["expected_shape"]
+    np.testing.assert_array_equal(out.toNumpy().reshape(-1), g["expected"])
+
+
+def test_fusion_cuda_graph_chain():
+    g = FUSION["fusion_cuda_graph_chain"]
+    x = arr(g["inputs"]["x"])
+
+    def chain(t):
+        for _ in range(160):
+            t = t + 1
+        return t
+
+    graph = Fusion.compile(chain, [x], cudaGraph=True)
+    np.testing.assert_array_equal(graph.run(x).toNumpy(), g["expected"])
+    np.testing.assert_array_equal(graph.run(arr(g["rebound"]["x"])).toNumpy(), g["expected_rebound"])
+    st = graph.getStats()
+    assert st["backend"] == "cuda-graph" and st["graphLaunches"] == 2
+    assert st["fusedKernels"] >= 1
+
+
+def test_fusion_precision_no_contraction():
+    g = FUSION["fusion_precision_no_contraction"]
+    a, b, c = (arr(g["inputs"][k]) for k in "abc")
+    eager = a + b * c
+    fused = Fusion.run(lambda: a + b * c)
+    assert bits(fused).tobytes() == bits(eager).tobytes()
+    # with contraction the result would be the exact product minus one
+    exact = np.float32(np.float64(np.float32(g["inputs"]["b"][0])) * np.float64(np.float32(g["inputs"]["c"][0])) - 1.0)
+    assert fused.toNumpy()[0] != exact
+
+
+# ----------------------------------------------------------- bitwise vs eager
+def rand(shape, seed, lo=-2.0, hi=2.0):
+    return np.random.default_rng(seed).uniform(lo, hi, shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16", "float16", "float64"])
+def test_tanh_x_plus_y_z_matches_eager_bitwise(dtype):
+    x = CudaArray.fromNumpy(rand((256, 1024), 1), dtype)
+    y = CudaArray.fromNumpy(rand((1024,), 2), dtype)
+    z = CudaArray.fromNumpy(rand((256, 1024), 3), dtype)
+    graph = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z], cudaGraph=True)
+    fused = graph.run(x, y, z)
+    eager = (x + y * z).tanh()
+    assert fused.getDtype() == dtype
+    assert bits(fused).tobytes() == bits(eager).tobytes()
+    assert graph.getStats()["fusedKernels"] == 1
+    assert [s["kind"] for s in graph.getPlan()] == ["kernel"]
+
+
+def test_tanh_x_plus_y_z_vs_oracle():
+    xs, ys, zs = rand((64, 512), 4), rand((512,), 5), rand((64, 512), 6)
+    x, y, z = (CudaArray.fromNumpy(v) for v in (xs, ys, zs))
+    out = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z]).run(x, y, z).toNumpy()
+    mul = O.binary(ys, 0, zs, 0, "MUL", 0)
+    add = O.binary(xs, 0, mul, 0, "ADD", 0)
+    ref = O.unary(add, 0, "TANH")
+    # a+b*c exact per op; tanh device vs libm within 4 ulp
+    d = np.abs(out.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert d.max() <= 4
+
+
+def test_strided_and_broadcast_leaves_bitwise():
+    base = CudaArray.fromNumpy(rand((96, 130), 7))
+    v = base.transpose()                  # [130, 96] strided leaf
+    w = CudaArray.fromNumpy(rand((130, 1), 8))
+    s = CudaArray.fromNumpy(rand((96,), 9))
+    fn = lambda a, b, c: ((a - b) / (c * c + 1.5)).exp() - a.sin() * 0.25  # noqa: E731
+    graph = Fusion.compile(fn, [v, w, s])
+    fused = graph.run(v, w, s)
+    assert bits(fused).tobytes() == bits(fn(v, w, s)).tobytes()
+
+
+def test_integer_and_compare_fusion_bitwise():
+    a = CudaArray.fromNumpy(np.arange(-50, 50, dtype=np.int32).reshape(10, 10))
+    b = CudaArray.fromNumpy(np.array([3, -2, 0, 7, 1, 5, -9, 2, 4, 6], np.int32))
+    for fn in (lambda p, q: CudaArray.where(p.gt(q), p * 2 + q, p * 3 - q),
+               lambda p, q: p / q + 1,
+               lambda p, q: (p * 7 - q).maximum(q) * p.le(q)):
+        fused = Fusion.compile(fn, [a, b]).run(a, b)
+        eager = fn(a, b)
+        assert fused.getDtype() == eager.getDtype()
+        np.testing.assert_array_equal(fused.toBits(), eager.toBits())
+
+
+def test_native_boundaries_inside_plan():
+    r = np.random.default_rng(10)
+    a = CudaArray.fromNumpy(r.integers(-3, 4, (64, 48)).astype(np.float32))
+    w = CudaArray.fromNumpy(r.integers(-3, 4, (48, 32)).astype(np.float32))
+    bias = CudaArray.fromNumpy(r.integers(-3, 4, (32,)).astype(np.float32))
+
+    def fn(x, m, b):
+        h = x.matmul(m) + b
+        h = CudaArray.where(h.gt(0), h, h * 0)
+        return [h, h.sum(1) * 0.5, h.softmax(-1)]
+
+    graph = Fusion.compile(fn, [a, w, bias])
+    outs = graph.run(a, w, bias)
+    eager = fn(a, w, bias)
+    for f, e in zip(outs, eager):
+        assert bits(f).tobytes() == bits(e).tobytes()
+    kinds = [s["kind"] for s in graph.getPlan()]
+    assert "native" in kinds and "kernel" in kinds
+    assert graph.getStats()["boundaries"] >= 3
+
+
+def test_run_async_and_wait():
+    x = CudaArray.fromNumpy(rand((512, 512), 11))
+    graph = Fusion.compile(lambda a: a * a + 1, [x], cudaGraph=True)
+    ex = graph.runAsync(x)
+    out = ex.wait()
+    assert ex.isFinished()
+    assert ex.wait() is out
+    np.testing.assert_array_equal(out.toNumpy(), (x * x + 1).toNumpy())
+
+
+def test_fusion_run_disabled_is_eager():
+    x = CudaArray.fromNumpy(rand((8,), 12))
+    out = Fusion.run(lambda: x + 1, enabled=False)
+    assert not out.isLazy()
+    np.testing.assert_array_equal(out.toNumpy(), (x + 1).toNumpy())
+
+
+def test_fusion_run_escaped_intermediate_is_materialized():
+    x = CudaArray.fromNumpy(rand((16,), 13))
+    kept = {}
+
+    def fn():
+        kept["mid"] = x * 2
+        return kept["mid"] + 1
+
+    out = Fusion.run(fn)
+    np.testing.assert_array_equal(kept["mid"].toNumpy(), (x * 2).toNumpy())
+    np.testing.assert_array_equal(out.toNumpy(), (x * 2 + 1).toNumpy())
+
+
+def test_compiled_graph_rejects_mismatched_inputs():
+    x = CudaArray.fromNumpy(rand((4, 4), 14))
+    graph = Fusion.compile(lambda a: a + 1, [x])
+    with pytest.raises(InvalidArgumentException):
+        graph.run(CudaArray.fromNumpy(rand((4, 5), 15)))
+    with pytest.raises(InvalidArgumentException):
+        graph.run(x, x)
+
+
+def test_module_cache_hits_on_identical_source():
+    Fusion.clearCache()
+    x = CudaArray.fromNumpy(rand((32,), 16))
+    Fusion.compile(lambda a: a * 3 - 1, [x])
+    st1 = Fusion.getCacheStats()
+    Fusion.compile(lambda a: a * 3 - 1, [x])
+    st2 = Fusion.getCacheStats()
+    assert st2["hits"] == st1["hits"] + 1
+    assert st2["entries"] == 1
+
+
+def test_graph_replays_all_match_eager_after_eager_work():
+    x = CudaArray.fromNumpy(rand((1000, 33), 17))
+    y = CudaArray.fromNumpy(rand((33,), 18))
+    graph = Fusion.compile(lambda a, b: (a * b + a).tanh(), [x, y], cudaGraph=True)
+    ref = bits((x * y + x).tanh()).tobytes()
+    for i in range(5):
+        _ = (x + float(i)).sum()      # eager work between replays
+        assert bits(graph.run(x, y)).tobytes() == ref
