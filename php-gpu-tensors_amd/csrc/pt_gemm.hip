@@ -284,6 +284,7 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
         lin = (lin % 8) * per + lin / 8;
     }
     const int bidx = (int)(lin / ntile);
+    if (bidx >= g.batch) return;  // whole workgroup: grid larger than the tile count
     const int t = (int)(lin % ntile);
     const int group = t / (GROUP_M * g.tiles_n);
     const int first_m = group * GROUP_M;
@@ -492,6 +493,11 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
                 break;
             }
         }
+        // the 256x128 kernel exists for one layout; the others run 128x128
+        // tiles, so the tile grid is recounted for that shape
+        g.tiles_m = (g.M + 127) / 128;
+        g.tiles_n = (g.N + 127) / 128;
+        g.remap = ((long long)g.tiles_m * g.tiles_n * g.batch) % 8 == 0;
         launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s);
         break;
     case TILE_128x128: launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s); break;

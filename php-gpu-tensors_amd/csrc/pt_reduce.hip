@@ -46,19 +46,32 @@ template <> struct RT<PT_FLOAT16> {
     __device__ static C cv(S s) { return f16_to_float(s); }
 };
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte chunk of a row.  Rows are read exactly once, so the loads are
+// nontemporal: on gfx950 that keeps the HBM stream at a higher rate than
+// cached loads (no L2 / Infinity Cache retention of dead lines).
 template <int DT, int V>
 __device__ __forceinline__ void load_chunk(const typename RT<DT>::S *p, typename RT<DT>::C (&v)[V])
 {
     using S = typename RT<DT>::S;
     if constexpr (V * sizeof(S) == 16) {
-        union { uint4 raw; S s[V]; } u;
-        u.raw = *(const uint4 *)p;
+        union { u32x4 raw; S s[V]; } u;
+        u.raw = __builtin_nontemporal_load((const u32x4 *)p);
 #pragma unroll
         for (int i = 0; i < V; i++) v[i] = RT<DT>::cv(u.s[i]);
     } else {
 #pragma unroll
         for (int i = 0; i < V; i++) v[i] = RT<DT>::cv(p[i]);
     }
+}
+
+// 16-byte nontemporal store of a register chunk (outputs written once).
+__device__ __forceinline__ void store16(void *dst, const void *src)
+{
+    u32x4 v;
+    memcpy(&v, src, 16);
+    __builtin_nontemporal_store(v, (u32x4 *)dst);
 }
 
 template <typename C> __device__ __forceinline__ C neg_inf();
@@ -217,38 +230,50 @@ __device__ __forceinline__ void store_out(void *out, int out_dt, size_t i, C v)
 }
 
 // ============================================================ row kernels
-// One wave64 per row; `rows_per_block` = blockDim.x / 64.  No LDS, no
-// block barrier: waves retire independently.
-template <int DT, int OP, int VEC>
+// WPR wave64s per row (1 or 4) and 256 / (64 * WPR) rows per 256-thread
+// block.  Each wave keeps 4 chunks of VEC elements in flight per lane;
+// with WPR = 4 the row's chunks interleave across the block's waves, so one
+// block streams a long row with 16 KiB in flight, and the four partial
+// states meet in LDS (ordered merge: argmax ties still go to the lowest
+// index).  With WPR = 1 there is no LDS and no barrier.
+template <typename T> struct LdsSlot {
+    __align__(16) unsigned char raw[sizeof(T)];
+};
+
+template <int DT, int OP, int VEC, int WPR>
 __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin, size_t rows,
                                                     int n, size_t ld, void *__restrict__ out,
                                                     int out_dt, int correction, int take_sqrt)
 {
     using S = typename RT<DT>::S;
     using C = typename RT<DT>::C;
+    constexpr int RPB = 4 / WPR;
     const int lane = threadIdx.x & 63;
-    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const int wave = threadIdx.x >> 6;
+    const int wr = wave % WPR;                        // wave within its row
+    const size_t row = (size_t)blockIdx.x * RPB + wave / WPR;
+    if (row >= rows) return;                          // uniform per block when WPR > 1
     const S *x = (const S *)xin + row * ld;
     Acc<C, OP> acc;
-    constexpr int STEP = 64 * VEC;
-    int i = lane * VEC;
+    constexpr int STEP = 64 * VEC;                    // one wave-wide chunk
+    constexpr int RSTEP = WPR * STEP;                 // one row-wide chunk
+    int i = wr * STEP + lane * VEC;
     // main loop: 4 chunks in flight per lane
-    for (; i + 3 * STEP + VEC <= n; i += 4 * STEP) {
+    for (; i + 3 * RSTEP + VEC <= n; i += 4 * RSTEP) {
         C v[4][VEC];
 #pragma unroll
-        for (int u = 0; u < 4; u++) load_chunk<DT, VEC>(x + i + u * STEP, v[u]);
+        for (int u = 0; u < 4; u++) load_chunk<DT, VEC>(x + i + u * RSTEP, v[u]);
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             if constexpr (OP == R_VAR) {
                 var_add_chunk<C, VEC>(acc, v[u], VEC);
             } else {
 #pragma unroll
-                for (int k = 0; k < VEC; k++) acc.add(v[u][k], i + u * STEP + k);
+                for (int k = 0; k < VEC; k++) acc.add(v[u][k], i + u * RSTEP + k);
             }
         }
     }
-    for (; i < n; i += STEP) {
+    for (; i < n; i += RSTEP) {
         C v[VEC];
         int valid = n - i < VEC ? n - i : VEC;
         if (valid == VEC) {
@@ -266,12 +291,30 @@ __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin
         Mom m = acc.lane_state();
 #pragma unroll
         for (int s = 32; s >= 1; s >>= 1) m = mom_combine(m, mom_shfl(m, s));
+        if constexpr (WPR > 1) {
+            __shared__ LdsSlot<Mom> part[4];
+            if (lane == 0) *reinterpret_cast<Mom *>(part[wave].raw) = m;
+            __syncthreads();
+            if (wr != 0) return;
+            for (int w = 1; w < WPR; w++) m = mom_combine(m, *reinterpret_cast<const Mom *>(part[wave + w].raw));
+        }
         if (lane == 0) {
             double var = m.m2 / (double)(n - correction);
             store_out(out, out_dt, row, take_sqrt ? sqrt(var) : var);
         }
     } else {
         wave_merge(acc);
+        if constexpr (WPR > 1) {
+            __shared__ LdsSlot<Acc<C, OP>> part[4];
+            if (lane == 0) memcpy(part[wave].raw, &acc, sizeof(acc));
+            __syncthreads();
+            if (wr != 0) return;
+            for (int w = 1; w < WPR; w++) {
+                Acc<C, OP> o;
+                memcpy(&o, part[wave + w].raw, sizeof(o));
+                acc.merge(o);
+            }
+        }
         if (lane == 0) {
             if constexpr (OP == R_ARGMAX || OP == R_ARGMIN) {
                 ((int32_t *)out)[row] = acc.i;
@@ -336,10 +379,10 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
 #pragma unroll
             for (int k = 0; k < VEC; k++) r[k] = (OS)(v[c][k] / sum);
             if constexpr (VEC * sizeof(OS) == 16) {
-                *(uint4 *)(y + i) = *(const uint4 *)r;
+                store16(y + i, r);
             } else if constexpr (VEC * sizeof(OS) == 32) {
-                ((uint4 *)(y + i))[0] = ((const uint4 *)r)[0];
-                ((uint4 *)(y + i))[1] = ((const uint4 *)r)[1];
+                store16(y + i, r);
+                store16((char *)(y + i) + 16, (const char *)r + 16);
             } else {
 #pragma unroll
                 for (int k = 0; k < VEC; k++) y[i + k] = r[k];
@@ -437,10 +480,10 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
         }
         if (i + VEC <= n) {
             if constexpr (VEC * sizeof(CT) == 16) {
-                *(uint4 *)(y + i) = *(const uint4 *)r;
+                store16(y + i, r);
             } else if constexpr (VEC * sizeof(CT) == 32) {
-                ((uint4 *)(y + i))[0] = ((const uint4 *)r)[0];
-                ((uint4 *)(y + i))[1] = ((const uint4 *)r)[1];
+                store16(y + i, r);
+                store16((char *)(y + i) + 16, (const char *)r + 16);
             } else {
 #pragma unroll
                 for (int k = 0; k < VEC; k++) y[i + k] = r[k];
@@ -940,11 +983,19 @@ static void launch_rows_t(const void *x, size_t rows, int n, size_t ld, void *ou
                           int correction, int take_sqrt, hipStream_t s)
 {
     constexpr int V = RT<DT>::V;
-    dim3 block(256), grid((unsigned)((rows + 3) / 4));
-    if (n % V == 0 && ld % V == 0 && aligned16(x))
-        k_row_reduce<DT, OP, V><<<grid, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
-    else
-        k_row_reduce<DT, OP, 1><<<grid, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+    dim3 block(256);
+    if (n % V == 0 && ld % V == 0 && aligned16(x)) {
+        // long rows: a block per row (16 chunks of 16 B in flight per row)
+        if (n >= 4 * 64 * V * 2)
+            k_row_reduce<DT, OP, V, 4><<<dim3((unsigned)rows), block, 0, s>>>(x, rows, n, ld, out, out_dt,
+                                                                              correction, take_sqrt);
+        else
+            k_row_reduce<DT, OP, V, 1><<<dim3((unsigned)((rows + 3) / 4)), block, 0, s>>>(
+                x, rows, n, ld, out, out_dt, correction, take_sqrt);
+    } else {
+        k_row_reduce<DT, OP, 1, 1><<<dim3((unsigned)((rows + 3) / 4)), block, 0, s>>>(x, rows, n, ld, out, out_dt,
+                                                                                       correction, take_sqrt);
+    }
 }
 
 template <int DT>

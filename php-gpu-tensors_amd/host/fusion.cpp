@@ -132,6 +132,7 @@ struct Kernel {
     bool affine = false;          // vectorizable (affine leaf maps)
     std::vector<LeafMap> leaf_maps;
     std::vector<bool> leaf_vec;   // leaf read as 4-vectors in the vector kernel
+    std::vector<bool> leaf_stream;  // leaf read once per element (nontemporal loads)
     pt_function_t fn_vec = nullptr;
     pt_function_t fn_scalar = nullptr;
 };
@@ -473,7 +474,9 @@ static void gather(const Plan &p, Kernel &k, int id, const CoordMap &cm, bool &a
 static void emit_prelude(std::ostringstream &os)
 {
     // hipRTC provides the HIP device builtins and vector types itself
-    os << "__device__ __forceinline__ float pt_b2f(unsigned short b){return __uint_as_float(((unsigned)b)<<16);}\n"
+    os << "typedef unsigned int pt_u4 __attribute__((ext_vector_type(4)));\n"
+          "typedef unsigned int pt_u2 __attribute__((ext_vector_type(2)));\n"
+          "__device__ __forceinline__ float pt_b2f(unsigned short b){return __uint_as_float(((unsigned)b)<<16);}\n"
           "__device__ __forceinline__ unsigned short pt_f2b(float f){unsigned u=__float_as_uint(f);"
           "if((u&0x7f800000u)==0x7f800000u&&(u&0x7fffffu))return (unsigned short)((u>>16)|0x40u);"
           "return (unsigned short)((u+0x7fffu+((u>>16)&1u))>>16);}\n"
@@ -582,11 +585,24 @@ static void emit_general(Plan &p, Kernel &k, std::ostringstream &os)
 }
 
 // Vector path: coordinates decoded once per group of 4 output elements.
+// Leaves that stream (read once per output element) and the outputs use
+// nontemporal 16-byte / 8-byte accesses so that they do not displace the
+// broadcast operands from L2 and the Infinity Cache.
+static std::string bits_to_ctype(int dt, const std::string &raw)
+{
+    switch (dt) {
+    case PT_FLOAT32: return "__uint_as_float(" + raw + ")";
+    case PT_FLOAT16: return "pt_h2f((unsigned short)(" + raw + "))";
+    case PT_BFLOAT16: return "pt_b2f((unsigned short)(" + raw + "))";
+    default: return "static_cast<" + std::string(ctype(dt)) + ">(" + raw + ")";
+    }
+}
+
 static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
 {
     std::string params;
     for (size_t l = 0; l < k.leaves.size(); l++) params += "const void* __restrict__ p" + std::to_string(l) + ",";
-    os << "extern \"C\" __global__ void " << k.name << "_v(" << params;
+    os << "extern \"C\" __global__ void __launch_bounds__(256) " << k.name << "_v(" << params;
     for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
     const int nd = k.ndims;
     os << "){\nconst unsigned long long n4=" << k.total / 4 << "ULL;\n"
@@ -599,42 +615,44 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
         os << "const unsigned long long c" << d << "=(i0/" << div << "ULL)%" << k.shape[d] << "ULL;\n";
         div *= (unsigned long long)k.shape[d];
     }
+    const char *f[4] = {"x", "y", "z", "w"};
     // leaf loads: L<slot>_<j>
     for (size_t l = 0; l < k.leaves.size(); l++) {
         const LeafMap &m = k.leaf_maps[l];
         int id = k.leaves[l];
         const Tensor &t = *p.items[id].t;
         std::string st = storage_type(t.dtype);
+        std::string L = "L" + std::to_string(l);
         os << "const unsigned long long o" << l << "=" << m.offset << "ULL";
         for (int d = 0; d < nd; d++)
             if (m.stride[d]) os << "+c" << d << "*" << m.stride[d] << "ULL";
         os << ";\n";
         std::string base = "static_cast<const " + st + "*>(p" + std::to_string(l) + ")";
+        std::string at = base + "+o" + std::to_string(l);
         long long inner = nd ? m.stride[nd - 1] : 0;
+        size_t es = dtype_size(t.dtype);
+        bool nt = k.leaf_stream[l];
         if (inner == 0) {
-            os << "const " << ctype(t.dtype) << " L" << l << "=" << load_conv(t.dtype, base + "[o" + std::to_string(l) + "]")
+            os << "const " << ctype(t.dtype) << " " << L << "=" << load_conv(t.dtype, base + "[o" + std::to_string(l) + "]")
                << ";\n";
             for (int j = 0; j < 4; j++)
-                os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "=L" << l << ";\n";
-        } else if (inner == 1 && k.leaf_vec[l]) {
-            size_t es = dtype_size(t.dtype);
-            if (es == 4) {
-                os << "const uint4 R" << l << "=*reinterpret_cast<const uint4*>(" << base << "+o" << l << ");\n";
-                const char *f[4] = {"x", "y", "z", "w"};
-                for (int j = 0; j < 4; j++) {
-                    std::string raw = std::string("R") + std::to_string(l) + "." + f[j];
-                    std::string v = t.dtype == PT_FLOAT32 ? "__uint_as_float(" + raw + ")"
-                                  : "static_cast<" + std::string(ctype(t.dtype)) + ">(" + raw + ")";
-                    os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "=" << v << ";\n";
-                }
-            } else {
-                for (int j = 0; j < 4; j++)
-                    os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "="
-                       << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j) + "]") << ";\n";
+                os << "const " << ctype(t.dtype) << " " << L << "_" << j << "=" << L << ";\n";
+        } else if (inner == 1 && k.leaf_vec[l] && es == 4) {
+            std::string ptr = "reinterpret_cast<const pt_u4*>(" + at + ")";
+            os << "const pt_u4 R" << l << "=" << (nt ? "__builtin_nontemporal_load(" + ptr + ")" : "*" + ptr) << ";\n";
+            for (int j = 0; j < 4; j++)
+                os << "const " << ctype(t.dtype) << " " << L << "_" << j << "="
+                   << bits_to_ctype(t.dtype, "R" + std::to_string(l) + "." + f[j]) << ";\n";
+        } else if (inner == 1 && k.leaf_vec[l] && es == 2) {
+            std::string ptr = "reinterpret_cast<const pt_u2*>(" + at + ")";
+            os << "const pt_u2 R" << l << "=" << (nt ? "__builtin_nontemporal_load(" + ptr + ")" : "*" + ptr) << ";\n";
+            for (int j = 0; j < 4; j++) {
+                std::string raw = "(R" + std::to_string(l) + "." + (j < 2 ? "x" : "y") + (j % 2 ? ">>16" : "&0xffffu") + ")";
+                os << "const " << ctype(t.dtype) << " " << L << "_" << j << "=" << bits_to_ctype(t.dtype, raw) << ";\n";
             }
         } else {
             for (int j = 0; j < 4; j++)
-                os << "const " << ctype(t.dtype) << " L" << l << "_" << j << "="
+                os << "const " << ctype(t.dtype) << " " << L << "_" << j << "="
                    << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j * inner) + "ULL]")
                    << ";\n";
         }
@@ -661,16 +679,29 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
             os << "const " << ctype(p.items[id].t->dtype) << " r" << r << "_" << j << "=" << val[id] << ";\n";
         }
     }
+    // outputs are contiguous and 16-byte aligned (checked at launch)
     for (size_t r = 0; r < k.roots.size(); r++) {
         const Tensor &t = *p.items[k.roots[r]].t;
         std::string st = storage_type(t.dtype);
-        if (t.dtype == PT_FLOAT32) {
-            os << "*reinterpret_cast<float4*>(static_cast<float*>(out" << r << ")+i0)=make_float4(r" << r
-               << "_0,r" << r << "_1,r" << r << "_2,r" << r << "_3);\n";
+        std::string rv = "r" + std::to_string(r) + "_";
+        std::string out = "static_cast<" + st + "*>(out" + std::to_string(r) + ")+i0";
+        size_t es = dtype_size(t.dtype);
+        auto bits = [&](int j) {
+            std::string v = rv + std::to_string(j);
+            if (t.dtype == PT_FLOAT32) return "__float_as_uint(" + v + ")";
+            if (es == 4) return "static_cast<unsigned int>(" + v + ")";
+            return "(unsigned int)(unsigned short)(" + store_conv(t.dtype, v) + ")";
+        };
+        if (es == 4) {
+            os << "__builtin_nontemporal_store((pt_u4){" << bits(0) << "," << bits(1) << "," << bits(2) << ","
+               << bits(3) << "},reinterpret_cast<pt_u4*>(" << out << "));\n";
+        } else if (es == 2) {
+            os << "__builtin_nontemporal_store((pt_u2){" << bits(0) << "|(" << bits(1) << "<<16)," << bits(2) << "|("
+               << bits(3) << "<<16)},reinterpret_cast<pt_u2*>(" << out << "));\n";
         } else {
             for (int j = 0; j < 4; j++)
                 os << "static_cast<" << st << "*>(out" << r << ")[i0+" << j << "]="
-                   << store_conv(t.dtype, "r" + std::to_string(r) + "_" + std::to_string(j)) << ";\n";
+                   << store_conv(t.dtype, rv + std::to_string(j)) << ";\n";
         }
     }
     os << "}}\n";
@@ -808,13 +839,21 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         }
         k.affine = affine && k.ndims > 0 && k.total % 4 == 0 && k.shape[k.ndims - 1] % 4 == 0;
         k.leaf_vec.assign(k.leaves.size(), false);
+        k.leaf_stream.assign(k.leaves.size(), false);
         if (k.affine) {
             for (size_t l = 0; l < k.leaves.size(); l++) {
                 const LeafMap &m = k.leaf_maps[l];
                 const Tensor &lt = *p->items[k.leaves[l]].t;
-                bool v = m.stride[k.ndims - 1] == 1 && dtype_size(lt.dtype) == 4 && m.offset % 4 == 0;
+                size_t es = dtype_size(lt.dtype);
+                bool v = m.stride[k.ndims - 1] == 1 && (es == 4 || es == 2) && m.offset % 4 == 0;
                 for (int d = 0; d < k.ndims - 1 && v; d++) v = m.stride[d] % 4 == 0;
                 k.leaf_vec[l] = v;
+                // a leaf that advances along every output dimension of
+                // extent > 1 is read exactly once per element
+                bool stream = true;
+                for (int d = 0; d < k.ndims; d++)
+                    if (k.shape[d] > 1 && m.stride[d] == 0) stream = false;
+                k.leaf_stream[l] = stream;
             }
             emit_vector(*p, k, os);
         }
@@ -878,8 +917,11 @@ static bool launch_kernel(Plan &p, Kernel &k, std::vector<TensorP> &vals)
     std::vector<void *> params;
     for (void *&ptr : ptrs) params.push_back(&ptr);
     size_t work = vec_ok ? k.total / 4 : k.total;
+    // one thread per work item: a full grid streams HBM faster on gfx950
+    // than a capped grid-stride loop (the loop remains for grids above the
+    // hardware limit)
     size_t blocks = (work + 255) / 256;
-    if (blocks > 256 * 32) blocks = 256 * 32;  // grid-stride beyond 32 workgroups per CU
+    if (blocks > 0x7fffffffu) blocks = 0x7fffffffu;
     return check_status(pt_launch(vec_ok ? k.fn_vec : k.fn_scalar, (unsigned)blocks, 256, params.data(),
                                   nullptr),
                         "Fusion kernel launch failed");

@@ -125,11 +125,14 @@ def test_arg_reduce_f32_vs_oracle(G, shape, op):
         assert np.array_equal(got, ref)
 
 
-def test_argmax_nan_inf_rules(G):
+@pytest.mark.parametrize("reps", [300, 1100])
+def test_argmax_nan_inf_rules(G, reps):
     inf, nan = np.inf, np.nan
     x = np.array([[nan, 1.0, 3.0, 3.0], [-inf, -inf, -inf, -inf], [nan] * 4,
                   [nan, -inf, 2.0, nan], [-inf, nan, -inf, 5.0]], np.float32)
-    x = np.tile(x, (1, 300))  # long rows: ties spread over lanes
+    # long rows: ties spread over lanes (and over the waves of a block when
+    # the row is long enough for the block-per-row kernel)
+    x = np.tile(x, (1, reps))
     got = G.arg_reduce(x, O.F32, "argmax", 1)
     assert np.array_equal(got, O.arg_reduce(x, O.F32, "argmax", 1))
     got = G.arg_reduce(-x, O.F32, "argmin", 1)
@@ -169,9 +172,12 @@ def test_reduce_transposed_view(G):
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
 @pytest.mark.parametrize("op", ["sum", "max", "argmax"])
-def test_low_precision_inputs_promote_to_f32(G, dt, op):
+@pytest.mark.parametrize("shape", [(48, 1024), (6, 8200)], ids=str)
+def test_low_precision_inputs_promote_to_f32(G, dt, op, shape):
     from phptensors import synthetic
-    x = synthetic.normal((48, 1024), 0.0, 1.0, seed=400)
+    x = synthetic.normal(shape, 0.0, 1.0, seed=400)
+    if op == "argmax":
+        x = np.round(x * 8) / 8  # ties
     xs = O.to_storage(x, dt)
     if op == "argmax":
         assert np.array_equal(G.arg_reduce(xs, dt, op, 1), O.arg_reduce(xs, dt, op, 1))
