@@ -51,13 +51,14 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // 16-byte chunk of a row.  Rows are read exactly once, so the loads are
 // nontemporal: on gfx950 that keeps the HBM stream at a higher rate than
 // cached loads (no L2 / Infinity Cache retention of dead lines).
-template <int DT, int V>
+template <int DT, int V, bool NT = true>
 __device__ __forceinline__ void load_chunk(const typename RT<DT>::S *p, typename RT<DT>::C (&v)[V])
 {
     using S = typename RT<DT>::S;
     if constexpr (V * sizeof(S) == 16) {
         union { u32x4 raw; S s[V]; } u;
-        u.raw = __builtin_nontemporal_load((const u32x4 *)p);
+        if constexpr (NT) u.raw = __builtin_nontemporal_load((const u32x4 *)p);
+        else u.raw = *(const u32x4 *)p;
 #pragma unroll
         for (int i = 0; i < V; i++) v[i] = RT<DT>::cv(u.s[i]);
     } else {
@@ -66,12 +67,48 @@ __device__ __forceinline__ void load_chunk(const typename RT<DT>::S *p, typename
     }
 }
 
-// 16-byte nontemporal store of a register chunk (outputs written once).
+// 16-byte store of a register chunk.
 __device__ __forceinline__ void store16(void *dst, const void *src)
 {
     u32x4 v;
     memcpy(&v, src, 16);
-    __builtin_nontemporal_store(v, (u32x4 *)dst);
+    *(u32x4 *)dst = v;
+}
+
+// Row-wide sum / max over the WPR waves of one row (LDS when WPR > 1).
+// Every wave of the row returns the same value.
+template <typename C, int WPR>
+__device__ __forceinline__ C row_sum(C v, C *lds)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, PT_WAVE);
+    if constexpr (WPR > 1) {
+        const int wave = threadIdx.x >> 6, w0 = wave - wave % WPR;
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) lds[wave] = v;
+        __syncthreads();
+        v = lds[w0];
+        for (int w = 1; w < WPR; w++) v = v + lds[w0 + w];
+    }
+    return v;
+}
+
+template <typename C> __device__ __forceinline__ C fmax_any(C a, C b);
+
+template <typename C, int WPR>
+__device__ __forceinline__ C row_max(C v, C *lds)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmax_any(v, __shfl_xor(v, m, PT_WAVE));
+    if constexpr (WPR > 1) {
+        const int wave = threadIdx.x >> 6, w0 = wave - wave % WPR;
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) lds[wave] = v;
+        __syncthreads();
+        v = lds[w0];
+        for (int w = 1; w < WPR; w++) v = fmax_any(v, lds[w0 + w]);
+    }
+    return v;
 }
 
 template <typename C> __device__ __forceinline__ C neg_inf();
@@ -79,6 +116,8 @@ template <> __device__ __forceinline__ float neg_inf<float>() { return -INFINITY
 template <> __device__ __forceinline__ double neg_inf<double>() { return -INFINITY; }
 
 __device__ __forceinline__ float fmax_c(float a, float b) { return fmaxf(a, b); }
+template <> __device__ __forceinline__ float fmax_any<float>(float a, float b) { return fmaxf(a, b); }
+template <> __device__ __forceinline__ double fmax_any<double>(double a, double b) { return fmax(a, b); }
 __device__ __forceinline__ double fmax_c(double a, double b) { return fmax(a, b); }
 __device__ __forceinline__ float fmin_c(float a, float b) { return fminf(a, b); }
 __device__ __forceinline__ double fmin_c(double a, double b) { return fmin(a, b); }
@@ -327,57 +366,60 @@ __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin
     }
 }
 
-// Fused softmax over register-resident rows: NCH chunks of VEC elements per
-// lane cover the row (n <= 64 * VEC * NCH).  One HBM read, one write.
-// y = exp(x - max) / sum(exp(x - max)): true division as the composite's
-// OP_DIV (cuda_array_ce.c:1995).
-template <int DT, int VEC, int NCH, typename OS>
-__global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xin, size_t rows,
-                                                     int n, size_t ld, OS *__restrict__ out)
+// ------------------------------------------------ register-resident rows
+// A row is split over WPR waves (1 or 4); lane `lane` of wave `wr` holds
+// NCH chunks of VEC elements, chunk c starting at element
+// ((c * WPR + wr) * 64 + lane) * VEC, so the block's loads of one chunk step
+// are contiguous.  Lanes whose last chunk lies inside the row (all lanes of
+// a row that is a multiple of the chunk layout) take branch-free paths so
+// that their NCH loads issue back to back.
+template <int VEC, int WPR>
+__device__ __forceinline__ int chunk_start(int c, int wr, int lane)
 {
-    using S = typename RT<DT>::S;
-    using C = typename RT<DT>::C;
-    const int lane = threadIdx.x & 63;
-    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const S *x = (const S *)xin + row * ld;
-    OS *y = out + row * (size_t)n;
-    C v[NCH][VEC];
-    C m = neg_inf<C>();
+    return ((c * WPR + wr) * 64 + lane) * VEC;
+}
+
+template <int DT, int VEC, int NCH, int WPR, bool NT, typename CT>
+__device__ __forceinline__ bool load_row(const typename RT<DT>::S *x, int n, int wr, int lane, CT pad,
+                                         CT (&v)[NCH][VEC])
+{
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    if (full) {
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-        if (i + VEC <= n) {
-            load_chunk<DT, VEC>(x + i, v[c]);
-        } else {
+        for (int c = 0; c < NCH; c++) {
+            typename RT<DT>::C t[VEC];
+            load_chunk<DT, VEC, NT>(x + chunk_start<VEC, WPR>(c, wr, lane), t);
 #pragma unroll
-            for (int k = 0; k < VEC; k++) v[c][k] = i + k < n ? RT<DT>::cv(x[i + k]) : neg_inf<C>();
+            for (int k = 0; k < VEC; k++) v[c][k] = (CT)t[k];
         }
+    } else {
 #pragma unroll
-        for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
-    }
+        for (int c = 0; c < NCH; c++) {
+            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+            if (i + VEC <= n) {
+                typename RT<DT>::C t[VEC];
+                load_chunk<DT, VEC, NT>(x + i, t);
 #pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) m = fmax_c(m, __shfl_xor(m, s, PT_WAVE));
-    C sum = 0;
+                for (int k = 0; k < VEC; k++) v[c][k] = (CT)t[k];
+            } else {
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-#pragma unroll
-        for (int k = 0; k < VEC; k++) {
-            C e = i + k < n ? exp_c(v[c][k] - m) : (C)0;
-            v[c][k] = e;
-            sum = sum + e;
+                for (int k = 0; k < VEC; k++) v[c][k] = i + k < n ? (CT)RT<DT>::cv(x[i + k]) : pad;
+            }
         }
     }
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) sum = sum + __shfl_xor(sum, s, PT_WAVE);
+    return full;
+}
+
+template <int VEC, int NCH, int WPR, typename OS, typename CT>
+__device__ __forceinline__ void store_row(OS *y, int n, int wr, int lane, bool full, const CT (&v)[NCH][VEC])
+{
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-        if (i + VEC <= n) {
-            OS r[VEC];
+        const int i = chunk_start<VEC, WPR>(c, wr, lane);
+        OS r[VEC];
 #pragma unroll
-            for (int k = 0; k < VEC; k++) r[k] = (OS)(v[c][k] / sum);
+        for (int k = 0; k < VEC; k++) r[k] = (OS)v[c][k];
+        if (full || i + VEC <= n) {
             if constexpr (VEC * sizeof(OS) == 16) {
                 store16(y + i, r);
             } else if constexpr (VEC * sizeof(OS) == 32) {
@@ -389,9 +431,94 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
             }
         } else {
             for (int k = 0; k < VEC; k++)
-                if (i + k < n) y[i + k] = (OS)(v[c][k] / sum);
+                if (i + k < n) y[i + k] = r[k];
         }
     }
+}
+
+// Variance / standard deviation: exact two-pass form (mean, then the sum of
+// squared deviations from it) over the values held in registers.  Same
+// result definition as the Welford kernels (M2 / (n - correction), sqrt for
+// std), one HBM pass.
+template <int DT, int VEC, int NCH, int WPR>
+__global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xin, size_t rows, int n,
+                                                     size_t ld, void *__restrict__ out, int out_dt,
+                                                     int correction, int take_sqrt)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    __shared__ C lds[4];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, wr = wave % WPR;
+    const size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    if (row >= rows) return;  // WPR > 1: one row per block, never taken
+    const S *x = (const S *)xin + row * ld;
+    C v[NCH][VEC];
+    load_row<DT, VEC, NCH, WPR, true>(x, n, wr, lane, (C)0, v);
+    C s = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int k = 0; k < VEC; k++) s = s + v[c][k];
+    const C mean = row_sum<C, WPR>(s, lds) / (C)n;
+    C q = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            // v - v keeps infinities poisoning the result as in Welford
+            C d = i + k < n ? v[c][k] - mean + (v[c][k] - v[c][k]) : (C)0;
+            q = q + d * d;
+        }
+    }
+    q = row_sum<C, WPR>(q, lds);
+    if (wr == 0 && lane == 0) {
+        double var = (double)q / (double)(n - correction);
+        store_out(out, out_dt, row, take_sqrt ? sqrt(var) : var);
+    }
+}
+
+// Fused softmax: y = exp(x - max) / sum(exp(x - max)), true division as the
+// composite's OP_DIV (cuda_array_ce.c:1995).  One HBM read, one write.
+template <int DT, int VEC, int NCH, int WPR, typename OS>
+__global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xin, size_t rows,
+                                                     int n, size_t ld, OS *__restrict__ out)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    __shared__ C lds[4];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, wr = wave % WPR;
+    const size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    if (row >= rows) return;  // WPR > 1: one row per block, never taken
+    const S *x = (const S *)xin + row * ld;
+    OS *y = out + row * (size_t)n;
+    C v[NCH][VEC];
+    const bool full = load_row<DT, VEC, NCH, WPR, false>(x, n, wr, lane, neg_inf<C>(), v);
+    C m = neg_inf<C>();
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
+    m = row_max<C, WPR>(m, lds);
+    C sum = 0;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+        for (int k = 0; k < VEC; k++) {
+            C e = (full || i + k < n) ? exp_c(v[c][k] - m) : (C)0;
+            v[c][k] = e;
+            sum = sum + e;
+        }
+    }
+    sum = row_sum<C, WPR>(sum, lds);
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
+    store_row<VEC, NCH, WPR>(y, n, wr, lane, full, v);
 }
 
 // 16-byte-aligned vector load of VEC values (VEC * sizeof(T) a multiple of 16).
@@ -407,91 +534,75 @@ __device__ __forceinline__ void load_vec16(const T *p, T (&v)[VEC])
     for (int k = 0; k < VEC; k++) v[k] = u.t[k];
 }
 
-// Fused layerNorm over register-resident rows (cuda_array_ce.c:2295-2323):
-// mean, centered, biased variance of the centered values, eps inside the
-// sqrt, true division, then gamma and beta.
-template <int DT, int VEC, int NCH, typename CT>
+// Fused layerNorm (cuda_array_ce.c:2295-2323): mean, centered, biased
+// variance of the centered values, eps inside the sqrt, true division, then
+// gamma and beta (contiguous [n] arrays).  With WPR = 4 a block walks the
+// rows blockIdx.x, blockIdx.x + gridDim.x, ... and keeps its gamma / beta
+// chunks in registers across them, so they are read once per block instead
+// of once per row.
+template <int DT, int VEC, int NCH, int WPR, typename CT>
 __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ xin, size_t rows,
                                                        int n, CT eps, const CT *__restrict__ gamma,
                                                        const CT *__restrict__ beta,
                                                        CT *__restrict__ out)
 {
     using S = typename RT<DT>::S;
+    __shared__ CT lds[4];
     const int lane = threadIdx.x & 63;
-    const size_t row = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const S *x = (const S *)xin + row * (size_t)n;
-    CT *y = out + row * (size_t)n;
-    CT v[NCH][VEC];
-    CT s = 0;
+    const int wave = threadIdx.x >> 6, wr = wave % WPR;
+    size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    const size_t row_step = WPR > 1 ? (size_t)gridDim.x : rows;
+    if (row >= rows) return;  // WPR > 1: uniform per block
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    CT g[NCH][VEC], b[NCH][VEC];
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-        if (i + VEC <= n) {
-            typename RT<DT>::C t[VEC];
-            load_chunk<DT, VEC>(x + i, t);
-#pragma unroll
-            for (int k = 0; k < VEC; k++) v[c][k] = (CT)t[k];
-        } else {
-#pragma unroll
-            for (int k = 0; k < VEC; k++) v[c][k] = i + k < n ? (CT)RT<DT>::cv(x[i + k]) : (CT)0;
-        }
-#pragma unroll
-        for (int k = 0; k < VEC; k++) s = s + v[c][k];
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) s = s + __shfl_xor(s, m, PT_WAVE);
-    const CT mean = s / (CT)n;
-    CT q = 0;
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-#pragma unroll
-        for (int k = 0; k < VEC; k++) {
-            CT d = i + k < n ? v[c][k] - mean : (CT)0;
-            v[c][k] = d;
-            q = q + d * d;
-        }
-    }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) q = q + __shfl_xor(q, m, PT_WAVE);
-    const CT dev = sqrt_c(q / (CT)n + eps);
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        int i = (c * 64 + lane) * VEC;
-        CT r[VEC];
-        CT g[VEC], b[VEC];
-        // gamma/beta follow x's chunk layout: vector loads, L2-resident
-        if (i + VEC <= n) {
-            if (gamma) load_vec16<CT, VEC>(gamma + i, g);
-            if (beta) load_vec16<CT, VEC>(beta + i, b);
+        const int i = chunk_start<VEC, WPR>(c, wr, lane);
+        if (full || i + VEC <= n) {
+            if (gamma) load_vec16<CT, VEC>(gamma + i, g[c]);
+            if (beta) load_vec16<CT, VEC>(beta + i, b[c]);
         } else {
             for (int k = 0; k < VEC; k++) {
-                g[k] = gamma && i + k < n ? gamma[i + k] : (CT)1;
-                b[k] = beta && i + k < n ? beta[i + k] : (CT)0;
+                g[c][k] = gamma && i + k < n ? gamma[i + k] : (CT)1;
+                b[c][k] = beta && i + k < n ? beta[i + k] : (CT)0;
             }
         }
+    }
+    for (; row < rows; row += row_step) {
+        const S *x = (const S *)xin + row * (size_t)n;
+        CT *y = out + row * (size_t)n;
+        CT v[NCH][VEC];
+        load_row<DT, VEC, NCH, WPR, false>(x, n, wr, lane, (CT)0, v);
+        CT s = 0;
 #pragma unroll
-        for (int k = 0; k < VEC; k++) {
-            CT t = v[c][k] / dev;
-            if (gamma) t = t * g[k];
-            if (beta) t = t + b[k];
-            r[k] = t;
-        }
-        if (i + VEC <= n) {
-            if constexpr (VEC * sizeof(CT) == 16) {
-                store16(y + i, r);
-            } else if constexpr (VEC * sizeof(CT) == 32) {
-                store16(y + i, r);
-                store16((char *)(y + i) + 16, (const char *)r + 16);
-            } else {
+        for (int c = 0; c < NCH; c++)
 #pragma unroll
-                for (int k = 0; k < VEC; k++) y[i + k] = r[k];
+            for (int k = 0; k < VEC; k++) s = s + v[c][k];
+        const CT mean = row_sum<CT, WPR>(s, lds) / (CT)n;
+        CT q = 0;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                CT d = (full || i + k < n) ? v[c][k] - mean : (CT)0;
+                v[c][k] = d;
+                q = q + d * d;
             }
-        } else {
-            for (int k = 0; k < VEC; k++)
-                if (i + k < n) y[i + k] = r[k];
         }
+        q = row_sum<CT, WPR>(q, lds);
+        const CT dev = sqrt_c(q / (CT)n + eps);
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                CT t = v[c][k] / dev;
+                if (gamma) t = t * g[c][k];
+                if (beta) t = t + b[c][k];
+                v[c][k] = t;
+            }
+        }
+        store_row<VEC, NCH, WPR>(y, n, wr, lane, full, v);
     }
 }
 
@@ -984,6 +1095,25 @@ static void launch_rows_t(const void *x, size_t rows, int n, size_t ld, void *ou
 {
     constexpr int V = RT<DT>::V;
     dim3 block(256);
+    if constexpr (OP == R_VAR) {
+        // rows that fit in registers: two-pass moments, one block per row
+        int chunks = (n + 64 * V - 1) / (64 * V);
+        if (n % V == 0 && ld % V == 0 && aligned16(x) && chunks > 4) {
+            dim3 grid1((unsigned)rows);
+            if (chunks <= 8) {
+                k_row_moments<DT, V, 2, 4><<<grid1, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+                return;
+            }
+            if (chunks <= 16) {
+                k_row_moments<DT, V, 4, 4><<<grid1, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+                return;
+            }
+            if (chunks <= 32) {
+                k_row_moments<DT, V, 8, 4><<<grid1, block, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+                return;
+            }
+        }
+    }
     if (n % V == 0 && ld % V == 0 && aligned16(x)) {
         // long rows: a block per row (16 chunks of 16 B in flight per row)
         if (n >= 4 * 64 * V * 2)
@@ -1139,24 +1269,29 @@ static pt_status reduce_driver(const void *input, void *output, int dtype, int r
 }
 
 // ---------------------------------------------------- fused row launchers
+// Register-resident row kernels: rows of up to 4 chunks per lane run one
+// wave per row (4 rows per block); longer rows run one block of 4 waves per
+// row (more waves in flight per CU, and rows up to 64 * VEC * 16 * 4
+// elements stay in registers); beyond that the streaming kernels re-read.
 template <int DT, typename OS>
 static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS *y, hipStream_t s)
 {
     constexpr int V = RT<DT>::V;
-    dim3 block(256), grid((unsigned)((rows + 3) / 4));
+    constexpr bool narrow = sizeof(typename RT<DT>::C) == 4;
+    dim3 block(256), grid4((unsigned)((rows + 3) / 4)), grid1((unsigned)rows);
     bool vec = n % V == 0 && ld % V == 0 && aligned16(x) && aligned16(y);
     int chunks = (n + 64 * V - 1) / (64 * V);
     if (vec) {
         switch (chunks) {
-        case 1: k_row_softmax<DT, V, 1, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
-        case 2: k_row_softmax<DT, V, 2, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
-        case 3: case 4: k_row_softmax<DT, V, 4, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
-        case 5: case 6: case 7: case 8:
-            k_row_softmax<DT, V, 8, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 1: k_row_softmax<DT, V, 1, 1, OS><<<grid4, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 2: k_row_softmax<DT, V, 2, 1, OS><<<grid4, block, 0, s>>>(x, rows, n, ld, y); return;
+        case 3: case 4: k_row_softmax<DT, V, 4, 1, OS><<<grid4, block, 0, s>>>(x, rows, n, ld, y); return;
         default:
-            if (chunks <= 16 && sizeof(typename RT<DT>::C) == 4) {
-                k_row_softmax<DT, V, 16, OS><<<grid, block, 0, s>>>(x, rows, n, ld, y);
-                return;
+            if (chunks <= 8) { k_row_softmax<DT, V, 2, 4, OS><<<grid1, block, 0, s>>>(x, rows, n, ld, y); return; }
+            if (chunks <= 16) { k_row_softmax<DT, V, 4, 4, OS><<<grid1, block, 0, s>>>(x, rows, n, ld, y); return; }
+            if (chunks <= 32) { k_row_softmax<DT, V, 8, 4, OS><<<grid1, block, 0, s>>>(x, rows, n, ld, y); return; }
+            if constexpr (narrow) {
+                if (chunks <= 64) { k_row_softmax<DT, V, 16, 4, OS><<<grid1, block, 0, s>>>(x, rows, n, ld, y); return; }
             }
             break;
         }
@@ -1164,27 +1299,29 @@ static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS
     k_row_softmax_stream<DT, OS><<<(unsigned)rows, 256, 0, s>>>(x, n, ld, y);
 }
 
+static const int kLnBlocks = 256 * 8;
+
 template <int DT, typename CT>
 static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, const CT *g,
                                   const CT *b, CT *y, hipStream_t s)
 {
     constexpr int V = RT<DT>::V;
-    dim3 block(256), grid((unsigned)((rows + 3) / 4));
+    dim3 block(256), grid4((unsigned)((rows + 3) / 4)), grid1((unsigned)rows);
     bool vec = n % V == 0 && aligned16(x) && aligned16(y) && (!g || aligned16(g)) &&
                (!b || aligned16(b));
     int chunks = (n + 64 * V - 1) / (64 * V);
+    // block-per-row kernels walk rows: 8 blocks per CU share the rows
+    grid1 = dim3((unsigned)(rows < (size_t)kLnBlocks ? rows : (size_t)kLnBlocks));
     if (vec) {
         switch (chunks) {
-        case 1: k_row_layernorm<DT, V, 1, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
-        case 2: k_row_layernorm<DT, V, 2, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
-        case 3: case 4: k_row_layernorm<DT, V, 4, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
-        case 5: case 6: case 7: case 8:
-            k_row_layernorm<DT, V, 8, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 1: k_row_layernorm<DT, V, 1, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 2: k_row_layernorm<DT, V, 2, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
+        case 3: case 4: k_row_layernorm<DT, V, 4, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
         default:
-            if (chunks <= 16 && sizeof(CT) == 4) {
-                k_row_layernorm<DT, V, 16, CT><<<grid, block, 0, s>>>(x, rows, n, eps, g, b, y);
-                return;
-            }
+            if (chunks <= 8) { k_row_layernorm<DT, V, 2, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
+            if (chunks <= 16) { k_row_layernorm<DT, V, 4, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
+            // (gamma and beta stay in registers too: 8 chunks per lane at most)
+            if (chunks <= 32) { k_row_layernorm<DT, V, 8, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
             break;
         }
     }

@@ -235,7 +235,7 @@ def test_empty_axis_rules(G):
 
 
 # ------------------------------------------------------------------- moments
-@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (3, 70001)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (3, 70001), (7, 1280), (16, 8192), (5, 2052)], ids=str)
 def test_var_std_vs_oracle(G, shape):
     from phptensors import synthetic
     x = synthetic.normal(shape, 3.0, 2.0, seed=600)
@@ -254,6 +254,11 @@ def test_var_nonfinite_and_correction_errors(G):
     from phptensors._abi import InvalidArgumentException
     x = np.array([1.0, np.inf], np.float64)
     assert np.isnan(G.moments(x, O.F64)[0])
+    # long rows (register-resident two-pass kernel): infinities poison too
+    xl = np.ones((2, 4096), np.float32)
+    xl[0, 5] = np.inf
+    got = G.moments(xl, O.F32, 1)
+    assert np.isnan(got[0]) and got[1] == 0.0
     with pytest.raises(InvalidArgumentException):
         G.moments(np.zeros((0, 3), np.float32), O.F32)
     with pytest.raises(InvalidArgumentException):
@@ -261,7 +266,8 @@ def test_var_nonfinite_and_correction_errors(G):
 
 
 # ------------------------------------------------------------ softmax / norm
-@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (8, 3), (4, 20000), (16, 8192)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (8, 3), (4, 20000), (16, 8192), (7, 1280),
+                                   (8, 12288)], ids=str)
 def test_softmax_lastaxis_vs_oracle(G, shape):
     from phptensors import synthetic
     x = synthetic.normal(shape, 0.0, 1.0, seed=700)
@@ -324,7 +330,7 @@ def test_layernorm_golden(G, case):
         assert out.ravel().tolist() == case["expected"]
 
 
-@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (4, 20000), (100, 12)], ids=str)
+@pytest.mark.parametrize("shape", [(64, 4096), (33, 1000), (4, 20000), (100, 12), (7, 1280), (8, 12288)], ids=str)
 def test_layernorm_vs_oracle(G, shape):
     from phptensors import synthetic
     x = synthetic.normal(shape, 0.5, 2.0, seed=800)
