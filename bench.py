@@ -37,6 +37,17 @@ from phptensors import _abi as A  # noqa: E402
 from phptensors import synthetic  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+
+# HBM bytes per dispatch of each timed kernel: rocprofv3 --pmc FETCH_SIZE and
+# --pmc WRITE_SIZE passes over this script (--no-cpu --copy-calibration
+# --steps 2 --warmup 1), each scaled by what the counter reads for a 128 MiB
+# device copy (fetch x 2.0, write x 1.0).  Re-measured when a kernel changes.
+PMC_TRAFFIC_BYTES = {
+    "reduce:sum": 134_509_568, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
+    "reduce:argmax": 134_530_048, "reduce:var": 134_534_144, "reduce:softmax": 268_547_072,
+    "reduce:layernorm": 269_093_888, "fused:tanh_x_plus_y_z": 1_610_681_472,
+    "gemm:bf16": 1_088_142_656, "gemm:fp16": 1_080_996_864, "gemm:fp32": 6_814_353_280,
+}
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 MALL_BYTES = 256 << 20
 
@@ -269,25 +280,31 @@ def _to_bf16(x):
     return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
 
 
-def reduce_cpu_baseline():
+def reduce_cpu_baseline(min_seconds=10.0):
     """The oracle (scalar C restatement, 1 thread) on the full config-2 input."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     rows, n = 8192, 4096
     x = synthetic.normal((rows, n), 0.0, 1.0, seed=2)
     ones, zeros = np.ones(n, np.float32), np.zeros(n, np.float32)
+    # repeat the full step until about 10 s of single-core work have run
+    steps = 0
     t0 = time.perf_counter()
-    O.reduce(x, O.F32, "sum", 1)
-    O.reduce(x, O.F32, "mean", 1)
-    O.reduce(x, O.F32, "max", 1)
-    O.arg_reduce(x, O.F32, "argmax", 1)
-    O.moments(x, O.F32, 1)
-    O.softmax_lastaxis(x)
-    O.layernorm_lastaxis(x, 1e-5, ones, zeros)
-    dt = time.perf_counter() - t0
-    total_bytes = 5 * (x.nbytes + rows * 4) + 2 * 2 * x.nbytes
+    while True:
+        O.reduce(x, O.F32, "sum", 1)
+        O.reduce(x, O.F32, "mean", 1)
+        O.reduce(x, O.F32, "max", 1)
+        O.arg_reduce(x, O.F32, "argmax", 1)
+        O.moments(x, O.F32, 1)
+        O.softmax_lastaxis(x)
+        O.layernorm_lastaxis(x, 1e-5, ones, zeros)
+        steps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds or steps >= 64:
+            break
+    total_bytes = steps * (5 * (x.nbytes + rows * 4) + 2 * 2 * x.nbytes)
     return {"value": total_bytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": "full config-2 step (all 7 ops over X[8192,4096]) on one host core; "
+            "sample": f"{steps} full config-2 steps (all 7 ops over X[8192,4096]) on one host core; "
                       f"{dt:.2f} s", "seconds": dt}
 
 
@@ -348,14 +365,26 @@ def main():
     roofline = None
     if dom is not None:
         r = dom[2]
+        op = f"{dom[0]}:{dom[1]}"
         if "GB/s" in r:
-            roofline = {"bound": "hbm", "kernel": r["kernel"], "op": f"{dom[0]}:{dom[1]}",
+            roofline = {"bound": "hbm", "kernel": r["kernel"], "op": op,
                         "achieved": round(r["GB/s"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(r["GB/s"] / HBM_PEAK_GBS, 4), "traffic": None}
+                        "frac": round(r["GB/s"] / HBM_PEAK_GBS, 4),
+                        "traffic": PMC_TRAFFIC_BYTES.get(op)}
         else:
-            roofline = {"bound": "mfma", "kernel": r["kernel"], "op": f"{dom[0]}:{dom[1]}",
+            roofline = {"bound": "mfma", "kernel": r["kernel"], "op": op,
                         "achieved": round(r["TFLOP/s"], 1), "peak": r["peak"], "unit": "TFLOP/s",
-                        "frac": round(r["frac"], 4), "traffic": None}
+                        "frac": round(r["frac"], 4), "traffic": PMC_TRAFFIC_BYTES.get(op)}
+        roofline["traffic_unit"] = "bytes per launch (HBM, PMC)"
+    # every timed kernel against its own roofline
+    kernels = []
+    for fname, fam in fams.items():
+        for k, r in fam.get("ops", {}).items():
+            op = f"{fname}:{k}"
+            kernels.append({"op": op, "kernel": r["kernel"], "us": round(r["ms"] * 1e3, 2),
+                            "achieved": round(r.get("GB/s", r.get("TFLOP/s", 0.0)), 1),
+                            "unit": "GB/s" if "GB/s" in r else "TFLOP/s", "frac": round(r["frac"], 4),
+                            "traffic": PMC_TRAFFIC_BYTES.get(op)})
     fracs = [f["frac"] for f in fams.values()]
     value = 100.0 * sum(fracs) / len(fracs) if fracs else 0.0
     cpu = None
@@ -380,6 +409,7 @@ def main():
                    "families": sorted(fams)},
         "families": {k: {kk: vv for kk, vv in v.items()} for k, v in fams.items()},
         "roofline": roofline,
+        "kernels": kernels,
         "cpu_baseline": cpu,
         "wall_s": round(wall, 2),
     }

@@ -340,11 +340,25 @@ pt_status pt_memcpy_d2d(void *dst, const void *src, size_t bytes, pt_stream_t st
                      "device to device copy");
 }
 
+// Byte fill through a kernel rather than hipMemsetAsync, so that the call
+// records a kernel node when a caller captures it into a graph (memset
+// nodes have replayed wrongly after the first replay on this platform).
+__global__ __launch_bounds__(256) void k_memset_bytes(unsigned char *dst, unsigned char v, size_t n)
+{
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) dst[i] = v;
+}
+
 pt_status pt_memset(void *dst, int value, size_t bytes, pt_stream_t stream)
 {
     PT_TRY(ensure_init());
     if (!bytes) return PT_OK;
-    return check_hip(hipMemsetAsync(dst, value, bytes, stream_of(stream)), "hipMemsetAsync");
+    size_t blocks = (bytes + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    k_memset_bytes<<<(unsigned)blocks, 256, 0, stream_of(stream)>>>((unsigned char *)dst, (unsigned char)value,
+                                                                     bytes);
+    return check_hip(hipGetLastError(), "memset kernel launch");
 }
 
 pt_status pt_host_alloc_pinned(void **ptr, size_t bytes)
