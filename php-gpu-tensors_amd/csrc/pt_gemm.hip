@@ -410,6 +410,188 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
         }
 }
 
+// ------------------------------------------- direct-to-LDS 16-bit kernel
+// bf16 / fp16 GEMM for whole 256x256 tiles with K a multiple of 64 and
+// k-contiguous A.  Operands go from global memory straight into LDS with
+// global_load_lds_dwordx4 (no register staging): each such instruction
+// fills 1 KB of LDS, 16 bytes per lane at lane-consecutive addresses, and
+// the lane -> global address map applies an XOR swizzle so that the
+// fragment reads are free of bank conflicts:
+//   k-contiguous operand, row r of BK/8 16-byte chunks: physical chunk pc
+//     holds logical k chunk pc ^ swz_k(r);
+//   row-major B ([k][n], n contiguous), k-row r of 32 chunks: physical
+//     chunk pc holds logical n chunk pc ^ ((r & 3) << 2).
+// Row-major B fragments are read with ds_read_b64_tr_b16, the gfx950 LDS
+// transpose read: in each group of 16 lanes, lane i receives, for j = 0..3,
+// element (i % 4) of the 4 elements addressed by lane 4j + i/4.  Lane
+// 4j + q therefore addresses B[k + j][n + 4q .. n + 4q + 3], and two such
+// reads give a lane the 8 consecutive k of its MFMA B operand.
+// Those reads are issued as inline asm and waited for explicitly: the
+// compiler would otherwise wait for every in-flight LDS DMA load before
+// them.  The two LDS stages are separate arrays, so that the compiler can
+// tell the DMA writes into one stage from the fragment reads of the other.
+// 8 waves (2 x 4) with 128 x 64 wave tiles; BK = 64 in two stages: the
+// loads of step k+1 run while step k is on the matrix cores.
+#define PT_LDS_AS __attribute__((address_space(3)))
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz_k(int row, int cpr)
+{
+    return cpr == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+template <int DT, bool B_KC>
+__global__ __launch_bounds__(512, 1) void k_gemm_direct(GemmArgs g)
+{
+    using S = uint16_t;
+    constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 4;
+    constexpr int WTM = BM / WM, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
+    constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+    constexpr int CPR = BK / 8;           // 16-byte chunks per k-contiguous row
+    constexpr int RPI = 64 / CPR;         // such rows per load instruction
+    constexpr int NQ = A_ELEMS / 512 / 8; // load instructions per wave per operand
+    constexpr int GROUP_M = 4;
+    __shared__ __attribute__((aligned(1024))) S lds0[A_ELEMS + B_ELEMS];
+    __shared__ __attribute__((aligned(1024))) S lds1[A_ELEMS + B_ELEMS];
+
+    const int ntile = g.tiles_m * g.tiles_n;
+    long long lin = blockIdx.x;
+    if (g.remap) {
+        long long total = (long long)ntile * g.batch;
+        long long per = total / 8;
+        lin = (lin % 8) * per + lin / 8;
+    }
+    const int bidx = (int)(lin / ntile);
+    if (bidx >= g.batch) return;  // whole workgroup
+    const int t = (int)(lin % ntile);
+    const int group = t / (GROUP_M * g.tiles_n);
+    const int first_m = group * GROUP_M;
+    const int gsz = min(g.tiles_m - first_m, GROUP_M);
+    const int tm = first_m + (t % (GROUP_M * g.tiles_n)) % gsz;
+    const int tn = (t % (GROUP_M * g.tiles_n)) / gsz;
+    const int m0 = tm * BM, n0 = tn * BN;
+    long long oa, ob;
+    batch_offsets(g, bidx, oa, ob);
+    const S *A = (const S *)g.a + oa + (long long)m0 * g.a_sm;
+    const S *B = (const S *)g.b + ob + (B_KC ? (long long)n0 * g.b_sn : (long long)n0);
+    const long long lda = g.a_sm, ldb = B_KC ? g.b_sn : g.b_sk;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    auto issue = [&](int kt, S *buf) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int q4 = 0; q4 < NQ; q4++) {
+            const int q = wave * NQ + q4;
+            const int row = q * RPI + lane / CPR, pc = lane % CPR;
+            const S *src = A + (long long)row * lda + k0 + (pc ^ swz_k(row, CPR)) * 8;
+            __builtin_amdgcn_global_load_lds((const void *)src, (PT_LDS_AS void *)(buf + q * 512), 16, 0, 0);
+        }
+#pragma unroll
+        for (int q4 = 0; q4 < NQ; q4++) {
+            const int q = wave * NQ + q4;
+            const S *src;
+            if constexpr (B_KC) {
+                const int row = q * RPI + lane / CPR, pc = lane % CPR;
+                src = B + (long long)row * ldb + k0 + (pc ^ swz_k(row, CPR)) * 8;
+            } else {
+                const int row = q * 2 + (lane >> 5), pc = lane & 31;
+                src = B + (long long)(k0 + row) * ldb + (pc ^ ((row & 3) << 2)) * 8;
+            }
+            __builtin_amdgcn_global_load_lds((const void *)src, (PT_LDS_AS void *)(buf + A_ELEMS + q * 512), 16, 0,
+                                             0);
+        }
+    };
+
+    using Frag = typename FragT<DT>::type;
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    auto read_frags = [&](const S *buf, int slice, Frag (&fa)[TM], Frag (&fb)[TN]) {
+        const S *la = buf;
+        const S *lb = buf + A_ELEMS;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int row = wm * WTM + i * 32 + (lane & 31);
+            const int kc = slice * 2 + (lane >> 5);
+            fa[i] = *(const Frag *)(la + row * BK + (kc ^ swz_k(row, CPR)) * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            if constexpr (B_KC) {
+                const int row = wn * WTN + j * 32 + (lane & 31);
+                const int kc = slice * 2 + (lane >> 5);
+                fb[j] = *(const Frag *)(lb + row * BK + (kc ^ swz_k(row, CPR)) * 8);
+            } else {
+                const int grp = lane >> 4, s = lane & 15;
+                const int n = wn * WTN + j * 32 + (grp & 1) * 16 + 4 * (s & 3);
+                union { s16x4_t h[2]; Frag f; } u;
+#pragma unroll
+                for (int tt = 0; tt < 2; tt++) {
+                    const int kk = slice * 16 + (grp >> 1) * 8 + tt * 4 + (s >> 2);
+                    const S *p = lb + kk * BN + ((n >> 3) ^ ((kk & 3) << 2)) * 8 + (n & 7);
+                    const unsigned addr = (unsigned)(size_t)(PT_LDS_AS const S *)p;
+                    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(u.h[tt]) : "v"(addr));
+                }
+                fb[j] = u.f;
+            }
+        }
+    };
+    // completes the asm transpose reads of fb (and, conservatively, every
+    // LDS access of the wave) before fb is used
+    auto tr_wait = [&](Frag (&f)[TN]) {
+        if constexpr (!B_KC) {
+            static_assert(TN == 2, "wait operands");
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]));
+        }
+    };
+
+    const int KT = g.K / BK;
+    issue(0, lds0);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    Frag fa[2][TM], fb[2][TN];
+    auto step = [&](int kt, S *cur, S *nxt) {
+        if (kt + 1 < KT) issue(kt + 1, nxt);  // nxt was last read before the previous barrier
+        read_frags(cur, 0, fa[0], fb[0]);
+        tr_wait(fb[0]);
+#pragma unroll
+        for (int sl = 0; sl < BK / 16; sl++) {
+            if (sl + 1 < BK / 16) read_frags(cur, sl + 1, fa[(sl + 1) & 1], fb[(sl + 1) & 1]);
+            mfma_block<DT, TM, TN>(acc, fa[sl & 1], fb[sl & 1]);
+            __builtin_amdgcn_iglp_opt(1);
+            if (sl + 1 < BK / 16) tr_wait(fb[(sl + 1) & 1]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's DMA loads of step kt+1 have landed
+        __syncthreads();
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, lds0, lds1);
+        if (kt + 1 < KT) step(kt + 1, lds1, lds0);
+    }
+
+    char *Cb = (char *)g.c + (size_t)bidx * (size_t)g.M * (size_t)g.N * sizeof(S);
+    const int col_l = lane & 31;
+    const int row_l = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * WTN + j * 32 + col_l;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + wm * WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
+                store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
+            }
+        }
+}
+
 // ---------------------------------------------------------------- host side
 static int g_sched = 2;
 
@@ -466,12 +648,12 @@ static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, 
 enum GemmTile {
     TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
-    TILE_COUNT = 8
+    TILE_256x256_DIRECT = 8, TILE_COUNT = 9
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
     {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
-    {256, 256, 1}, {256, 256, 2}};
+    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}};
 
 static int g_tile_override = -1;
 
@@ -627,12 +809,43 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     int tile = g_tile_override;
     if (tile < 0) {
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
-        tile = (g.M >= 256 && g.N >= 256 && t256 >= 256) ? TILE_256x256
+        tile = (g.M >= 256 && g.N >= 256 && t256 >= 256) ? TILE_256x256_DIRECT
              : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
+    }
+    auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    if (tile == TILE_256x256_DIRECT) {
+        // direct-to-LDS kernel: 16-bit operands, whole 256x256 tiles, K a
+        // multiple of 64, k-contiguous A, B k- or n-contiguous, 16-byte
+        // aligned rows and batch offsets
+        const bool b_row = g.b_sn == 1, b_col = g.b_sk == 1;
+        const long long ldb = b_row ? g.b_sk : g.b_sn;
+        bool direct = dtype != PT_FLOAT32 && g.a_sk == 1 && (b_row || b_col) && g.M % 256 == 0 &&
+                      g.N % 256 == 0 && g.K % 64 == 0 && aligned(a) && aligned(b) && g.a_sm % 8 == 0 &&
+                      ldb % 8 == 0;
+        for (int d = 0; d < g.nbd; d++)
+            if (g.bsa[d] % 8 || g.bsb[d] % 8) direct = false;
+        long long tiles = (long long)(g.M / 256) * (g.N / 256) * batch;
+        if (direct && tiles <= 0x7fffffffLL) {
+            g.tiles_m = g.M / 256;
+            g.tiles_n = g.N / 256;
+            g.remap = tiles % 8 == 0;
+            dim3 grid((unsigned)tiles), block(512);
+            if (dtype == PT_BFLOAT16) {
+                if (b_row) k_gemm_direct<PT_BFLOAT16, false><<<grid, block, 0, s>>>(g);
+                else k_gemm_direct<PT_BFLOAT16, true><<<grid, block, 0, s>>>(g);
+            } else {
+                if (b_row) k_gemm_direct<PT_FLOAT16, false><<<grid, block, 0, s>>>(g);
+                else k_gemm_direct<PT_FLOAT16, true><<<grid, block, 0, s>>>(g);
+            }
+            PT_LAUNCH_CHECK("matmul");
+            counters().mfma_gemm_calls++;
+            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s", "mfma-direct-lds");
+            return PT_OK;
+        }
+        tile = TILE_256x256;
     }
     int bm = kTiles[tile].bm, bn = kTiles[tile].bn;
     const int BK = (dtype == PT_FLOAT32 ? 16 : 32) * kTiles[tile].kmul;
-    auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     bool vec_ok = aligned(a) && aligned(b);
     // vector (unchecked) loads need whole tiles, 16-byte aligned rows and
     // batch offsets that keep that alignment

@@ -72,7 +72,7 @@ def _ints(shape, seed, lo=-8, hi=8):
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8])
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bmnk", SHAPES, ids=str)
 def test_matmul_integer_exact(A, bmnk, dt, tile):
@@ -83,6 +83,49 @@ def test_matmul_integer_exact(A, bmnk, dt, tile):
     a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
     got = run(A, a, b, dt)
     assert np.array_equal(got, ref(a, b, dt))
+
+
+@pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
+@pytest.mark.parametrize("bmnk", [(1, 512, 256, 512), (2, 256, 512, 128), (3, 256, 256, 64),
+                                  (1, 256, 256, 96), (2, 768, 256, 192)], ids=str)
+def test_matmul_direct_lds_kernel(A, dt, layout, bmnk):
+    """Tile 8 (direct-to-LDS kernel, swizzled LDS, transpose reads for
+    row-major B): exact on integer-valued operands for row-major and
+    transposed B; shapes it does not take (K % 64 != 0, transposed A) run the
+    fallback tile and must agree too."""
+    A.load().pt_matmul_set_tile(8)
+    try:
+        b_, m, n, k = bmnk
+        a32 = _ints((b_, m, k), seed=m + k)
+        b32 = _ints((b_, k, n), seed=n + 2 * k)
+        a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+        expect = ref(a, b, dt)
+        kw = {}
+        a_in, b_in = a, b
+        if layout == "NT":   # B as the transposed view of a [b, n, k] buffer
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+            kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
+        if layout == "TN":   # A as the transposed view of a [b, k, m] buffer
+            a_in = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+            kw.update(shape_a=(b_, m, k), strides_a=[m * k, 1, m])
+        got = run(A, a_in, b_in, dt, **kw)
+        assert np.array_equal(got, expect)
+    finally:
+        A.load().pt_matmul_set_tile(-1)
+
+
+def test_matmul_direct_lds_batch_broadcast(A):
+    A.load().pt_matmul_set_tile(8)
+    try:
+        a = O.to_storage(_ints((1, 256, 128), seed=7), O.BF16)
+        b = O.to_storage(_ints((4, 128, 256), seed=8), O.BF16)
+        assert np.array_equal(run(A, a, b, O.BF16), ref(a, b, O.BF16))
+        a4 = O.to_storage(_ints((4, 256, 128), seed=9), O.BF16)
+        b2 = O.to_storage(_ints((128, 512), seed=10), O.BF16)
+        assert np.array_equal(run(A, a4, b2, O.BF16), ref(a4, b2, O.BF16))
+    finally:
+        A.load().pt_matmul_set_tile(-1)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
