@@ -234,8 +234,9 @@ const char *pt_matmul_precision_name(void);
  * cuda_blas_tune_matmul (matmul_kernels.h:34-38): 0 = 256x128, 1 = 128x128,
  * 2 = 64x64, 3 = 256x256 workgroup tiles, 5 = 256x256 with a doubled K
  * step, 8 = 256x256 direct-to-LDS kernel for f16/bf16 (whole tiles, K a
- * multiple of 64, k-contiguous A; other cases run tile 3), -1 = automatic
- * choice (default). */
+ * multiple of 64, k-contiguous A; other cases run tile 3), 9 = 256x128
+ * with 8 waves (the large-problem fp32 choice), -1 = automatic choice
+ * (default). */
 pt_status pt_matmul_set_tile(int tile);
 /* Instruction-schedule variant of the MFMA kernels (tuning knob):
  * 0 = compiler default, 1 and 2 = iglp strategies (2 is the default),

@@ -648,12 +648,12 @@ static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, 
 enum GemmTile {
     TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
-    TILE_256x256_DIRECT = 8, TILE_COUNT = 9
+    TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_COUNT = 10
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
     {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
-    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}};
+    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}};
 
 static int g_tile_override = -1;
 
@@ -685,6 +685,9 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
     case TILE_128x128: launch_layouts<DT, 128, 128, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     case TILE_256x256: launch_layouts<DT, 256, 256, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
     case TILE_256x256_K2: launch_layouts<DT, 256, 256, 2 * BK, 2, 4>(g, a_kc, b_kc, check, s); break;
+    // 8 waves on a 256x128 tile (128x32 per wave): the fp32 kernel that
+    // keeps its accumulators and staging in registers without spilling
+    case TILE_256x128_W8: launch_layouts<DT, 256, 128, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
     default: launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     }
 }
@@ -809,8 +812,9 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     int tile = g_tile_override;
     if (tile < 0) {
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
-        tile = (g.M >= 256 && g.N >= 256 && t256 >= 256) ? TILE_256x256_DIRECT
-             : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
+        tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
+                   ? (dtype == PT_FLOAT32 ? TILE_256x128_W8 : TILE_256x256_DIRECT)
+                   : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
     }
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     if (tile == TILE_256x256_DIRECT) {

@@ -72,7 +72,7 @@ def _ints(shape, seed, lo=-8, hi=8):
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9])
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bmnk", SHAPES, ids=str)
 def test_matmul_integer_exact(A, bmnk, dt, tile):
