@@ -274,6 +274,85 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
     return fam
 
 
+# ---------------------------------------------------------------- config 5
+def mlp_family(steps, warmup):
+    """MLP training step (784->1024->1024->10, batch 4096, softmax-CE,
+    backward, clip, AdamW) recorded once by Fusion.compile and replayed."""
+    from phptensors import CudaArray, mlp
+    from phptensors.optimizer import Optimizer
+    lib = A.load()
+    layers, rows = (784, 1024, 1024, 10), 4096
+    params = mlp.init_parameters(layers, 5)
+    x, y = mlp.synthetic_batch(rows, layers[0], layers[-1], 5)
+    xt, yt = CudaArray.fromNumpy(x), CudaArray.fromNumpy(y)
+    opt = Optimizer.adamW()
+    state = opt.initState(params)
+    rate = CudaArray.full([1], 1e-3)
+    inputs = mlp.training_inputs(xt, yt, rate, params, state)
+    graph = mlp.compile_training_plan(inputs, opt)
+    ev0, ev1 = ctypes.c_void_p(), ctypes.c_void_p()
+    A.check(lib.pt_event_create(ctypes.byref(ev0)), "event")
+    A.check(lib.pt_event_create(ctypes.byref(ev1)), "event")
+
+    def timed(count):
+        A.check(lib.pt_event_record(ev0, None), "record")
+        graph.replay(count, *inputs)
+        A.check(lib.pt_event_record(ev1, None), "record")
+        A.check(lib.pt_event_synchronize(ev1), "sync")
+        ms = ctypes.c_float()
+        A.check(lib.pt_event_elapsed_ms(ev0, ev1, ctypes.byref(ms)), "elapsed")
+        return ms.value / count
+
+    timed(max(1, warmup))
+    ms = timed(max(1, steps))
+    # eager: the same step through the Python-level autograd, synchronized
+    A.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(3):
+        out = mlp.train_batch(xt, yt, params, opt, state, rate)
+    out["loss"].item()
+    eager_ms = (time.perf_counter() - t0) / 3 * 1e3
+    lib.pt_event_destroy(ev0)
+    lib.pt_event_destroy(ev1)
+    flops = mlp.step_flops(rows, layers)
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"mlp step (compiled plan): {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s  {100 * tf / PEAK_TFLOPS['fp32']:.1f}% of fp32;"
+        f" eager {eager_ms * 1e3:.1f} us")
+    kinds = [s["kind"] for s in graph.getPlan()]
+    return {"workload": "config5: MLP 784-1024-1024-10 fp32, batch 4096, softmax-CE, backward, clip 5, AdamW 1e-3",
+            "ms_per_step": ms, "TFLOP/s": tf, "frac": tf / PEAK_TFLOPS["fp32"], "flop_per_step": flops,
+            "eager_ms_per_step": eager_ms, "plan_steps": len(kinds), "plan_native_steps": kinds.count("native"),
+            "plan_kernels": kinds.count("kernel")}
+
+
+def mlp_cpu_baseline(sample_rows=256):
+    """float64 numpy restatement of the step on a row sample, BLAS on one thread."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import mlp_ref as R
+    from phptensors import mlp
+    try:
+        from threadpoolctl import threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    layers = (784, 1024, 1024, 10)
+    params = [p.toNumpy().astype(np.float64) for p in mlp.init_parameters(layers, 5)]
+    x, y = mlp.synthetic_batch(sample_rows, layers[0], layers[-1], 5)
+    zeros = [np.zeros_like(p) for p in params]
+    ctx = threadpool_limits(limits=1) if threadpool_limits else None
+    try:
+        if ctx:
+            ctx.__enter__()
+        t0 = time.perf_counter()
+        R.train_step(x, y, params, zeros, zeros, 1.0, 1.0, 1e-3, mlp.DECAY_MASK)
+        dt = time.perf_counter() - t0
+    finally:
+        if ctx:
+            ctx.__exit__(None, None, None)
+    flops = mlp.step_flops(sample_rows, layers)
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"{sample_rows} of 4096 rows, float64 numpy step on one BLAS thread; {dt:.2f} s"}
+
+
 def _to_bf16(x):
     """float32 -> bfloat16 bits, round to nearest even (NaN-free input)."""
     u = x.view(np.uint32).astype(np.uint64)
@@ -323,7 +402,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="reduce,fused,gemm")
+    ap.add_argument("--only", default="reduce,fused,gemm,mlp")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 128 MiB device copy first (reference for PMC byte counters)")
@@ -354,6 +433,10 @@ def main():
         fams["fused"] = fused_family(args.steps, args.warmup)
     if "gemm" in only:
         fams["gemm"] = gemm_family(args.steps, args.warmup)
+    # config 5 is reported beside the metric (it is not one of its families)
+    extra = {}
+    if "mlp" in only:
+        extra["mlp"] = mlp_family(max(1, args.steps // 2), args.warmup)
     wall = time.perf_counter() - t_wall
 
     # dominant kernel (largest time in a step) for the roofline object
@@ -396,6 +479,8 @@ def main():
             fams["fused"]["cpu_baseline"] = fused_cpu_baseline()
         if "gemm" in fams:
             fams["gemm"]["cpu_baseline"] = gemm_cpu_baseline()
+        if "mlp" in extra:
+            extra["mlp"]["cpu_baseline"] = mlp_cpu_baseline()
     ms_step = sum(f["ms_per_step"] for f in fams.values())
     line = {
         "metric": "GEMM TFLOP/s + reduce/fused-eltwise HBM GB/s, % of MI355X peak, 1 GPU",
@@ -410,6 +495,7 @@ def main():
         "families": {k: {kk: vv for kk, vv in v.items()} for k, v in fams.items()},
         "roofline": roofline,
         "kernels": kernels,
+        "config5_mlp": extra.get("mlp"),
         "cpu_baseline": cpu,
         "wall_s": round(wall, 2),
     }

@@ -12,6 +12,7 @@ import numbers
 import numpy as np
 
 from . import _abi, _host
+from . import autograd as AG
 from ._abi import InvalidArgumentException, RuntimeException  # noqa: F401
 
 GLOBAL_AXIS = -1000
@@ -83,10 +84,13 @@ def _ints(seq):
 class CudaArray:
     """GPU tensor handle (src/tensor.h tensor_t behind a CudaArray object)."""
 
-    __slots__ = ("_h", "__weakref__")
+    __slots__ = ("_h", "_rg", "_node", "_grad", "__weakref__")
 
     def __init__(self, data=None, dtype="float32"):
         self._h = None
+        self._rg = False
+        self._node = None
+        self._grad = None
         if data is None:
             return
         arr = np.asarray(data)
@@ -98,6 +102,9 @@ class CudaArray:
         _host.check_handle(handle, what)
         obj = cls.__new__(cls)
         obj._h = handle
+        obj._rg = False
+        obj._node = None
+        obj._grad = None
         return obj
 
     def __del__(self):
@@ -149,7 +156,15 @@ class CudaArray:
 
     @classmethod
     def where(cls, condition, x, y):
-        return cls._wrap(_host.load().phpt_where(condition._h, x._h, y._h), "where")
+        out = cls._wrap(_host.load().phpt_where(condition._h, x._h, y._h), "where")
+        if AG.active(x, y):
+            def back(g):
+                zero = g * 0.0
+                gx = AG.reduce_to(CudaArray.where(condition, g, zero), x.getShape()) if AG.needs_grad(x) else None
+                gy = AG.reduce_to(CudaArray.where(condition, zero, g), y.getShape()) if AG.needs_grad(y) else None
+                return [gx, gy]
+            AG.record(out, [x, y], back, "where")
+        return out
 
     # ------------------------------------------------------------ metadata
     def getShape(self):
@@ -226,9 +241,15 @@ class CudaArray:
         lib = _host.load()
         if isinstance(other, CudaArray):
             a, b = (other, self) if reverse else (self, other)
-            return CudaArray._wrap(lib.phpt_binary(a._h, b._h, op))
+            out = CudaArray._wrap(lib.phpt_binary(a._h, b._h, op))
+            if AG.active(a, b):
+                _record_binary(out, a, b, op)
+            return out
         v, iv, kind = _scalar_args(other)
-        return CudaArray._wrap(lib.phpt_scalar_op(self._h, v, iv, kind, op, 1 if reverse else 0))
+        out = CudaArray._wrap(lib.phpt_scalar_op(self._h, v, iv, kind, op, 1 if reverse else 0))
+        if AG.active(self):
+            _record_scalar(out, self, other, op, reverse)
+        return out
 
     def add(self, other):
         return self._binary(other, OP["ADD"])
@@ -305,7 +326,22 @@ class CudaArray:
         return self.matmul(other)
 
     def _unary(self, op):
-        return CudaArray._wrap(_host.load().phpt_unary(self._h, op))
+        out = CudaArray._wrap(_host.load().phpt_unary(self._h, op))
+        if AG.active(self):
+            x = self
+            if op == OP["EXP"]:
+                AG.record(out, [x], lambda g: [g * out], "exp")
+            elif op == OP["LOG"]:
+                AG.record(out, [x], lambda g: [g / x], "log")
+            elif op == OP["NEG"]:
+                AG.record(out, [x], lambda g: [-g], "neg")
+            elif op == OP["SQRT"]:
+                AG.record(out, [x], lambda g: [g / (out * 2.0)], "sqrt")
+            elif op == OP["TANH"]:
+                AG.record(out, [x], lambda g: [g * (1.0 - out * out)], "tanh")
+            else:
+                raise InvalidArgumentException("Backward is not implemented for this unary operation")
+        return out
 
     def sqrt(self): return self._unary(OP["SQRT"])
     def exp(self): return self._unary(OP["EXP"])
@@ -342,7 +378,10 @@ class CudaArray:
         return GLOBAL_AXIS if axis is None else int(axis)
 
     def _reduce(self, axis, op):
-        return CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), op))
+        out = CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), op))
+        if AG.active(self):
+            _record_reduce(out, self, axis, op)
+        return out
 
     def sum(self, axis=None): return self._reduce(axis, OP["SUM"])
     def mean(self, axis=None): return self._reduce(axis, OP["MEAN"])
@@ -374,21 +413,41 @@ class CudaArray:
     def matmul(self, other):
         if not isinstance(other, CudaArray):
             raise InvalidArgumentException("matmul() expects a CudaArray operand")
-        return CudaArray._wrap(_host.load().phpt_matmul(self._h, other._h))
+        out = CudaArray._wrap(_host.load().phpt_matmul(self._h, other._h))
+        if AG.active(self, other):
+            a, b = self, other
+
+            def back(g):
+                # upstream @ B^T and A^T @ upstream over transposed views (autograd.c:1539-1585)
+                ga = AG.reduce_to(g.matmul(b.swapaxes(-1, -2)), a.getShape()) if AG.needs_grad(a) else None
+                gb = AG.reduce_to(a.swapaxes(-1, -2).matmul(g), b.getShape()) if AG.needs_grad(b) else None
+                return [ga, gb]
+            AG.record(out, [a, b], back, "matmul")
+        return out
 
     # ------------------------------------------------------------ views
     def reshape(self, shape):
         sh, n = _ints(shape)
-        return CudaArray._wrap(_host.load().phpt_reshape(self._h, sh, n))
+        out = CudaArray._wrap(_host.load().phpt_reshape(self._h, sh, n))
+        if AG.active(self):
+            src = self.getShape()
+            AG.record(out, [self], lambda g: [g.reshape(src)], "reshape")
+        return out
 
     def flatten(self):
         return self.reshape([-1])
 
     def transpose(self, axis=None):
         nd = self.getNdims()
-        perm = list(range(nd))[::-1] if axis is None else list(axis)
+        perm = list(range(nd))[::-1] if axis is None else [a % nd for a in axis]
         p, n = _ints(perm)
-        return CudaArray._wrap(_host.load().phpt_transpose(self._h, p, n))
+        out = CudaArray._wrap(_host.load().phpt_transpose(self._h, p, n))
+        if AG.active(self):
+            inv = [0] * nd
+            for i, a in enumerate(perm):
+                inv[a] = i
+            AG.record(out, [self], lambda g: [g.transpose(inv)], "transpose")
+        return out
 
     @property
     def T(self):
@@ -403,7 +462,11 @@ class CudaArray:
 
     def broadcastTo(self, shape):
         sh, n = _ints(shape)
-        return CudaArray._wrap(_host.load().phpt_broadcast_to(self._h, sh, n))
+        out = CudaArray._wrap(_host.load().phpt_broadcast_to(self._h, sh, n))
+        if AG.active(self):
+            src = self.getShape()
+            AG.record(out, [self], lambda g: [AG.reduce_to(g, src)], "broadcast")
+        return out
 
     def slice(self, axis, start, stop, step=1):
         return CudaArray._wrap(_host.load().phpt_slice(self._h, int(axis), int(start), int(stop), int(step)))
@@ -428,6 +491,31 @@ class CudaArray:
             new = shape[:axis] + shape[axis + 1:]
         return self.reshape(new)
 
+    # ------------------------------------------------------------ autograd
+    def requiresGrad(self, requiresGrad=True):
+        """Mark a leaf for gradient accumulation (returns self)."""
+        if requiresGrad and self.getDtype() not in ("float32", "float64", "float16", "bfloat16"):
+            raise InvalidArgumentException("Only floating tensors can require gradients")
+        self._rg = bool(requiresGrad)
+        return self
+
+    def backward(self, gradient=None, retainGraph=False):
+        if not AG.needs_grad(self):
+            raise RuntimeException("backward() on a tensor that does not require gradients")
+        AG.backward(self, gradient)
+        if not retainGraph:
+            self._node = None
+
+    def grad(self):
+        return self._grad
+
+    def zeroGrad(self):
+        self._grad = None
+
+    def detach(self):
+        """Same values, no history (a new handle on the same storage)."""
+        return CudaArray._wrap(_host.load().phpt_retain(self._h))
+
     def __repr__(self):
         return f"CudaArray(shape={self.getShape()}, dtype={self.getDtype()})"
 
@@ -447,3 +535,61 @@ def _from_numpy(arr, code):
     else:
         h = _from_bits(arr.astype(NUMPY_OF[code], copy=False), code)
     return _host.check_handle(h, "upload")
+
+
+# ------------------------------------------------------------ gradient recorders
+def _record_binary(out, a, b, op):
+    if op == OP["ADD"]:
+        back = lambda g: [AG.reduce_to(g, a.getShape()) if AG.needs_grad(a) else None,  # noqa: E731
+                          AG.reduce_to(g, b.getShape()) if AG.needs_grad(b) else None]
+    elif op == OP["SUB"]:
+        back = lambda g: [AG.reduce_to(g, a.getShape()) if AG.needs_grad(a) else None,  # noqa: E731
+                          AG.reduce_to(-g, b.getShape()) if AG.needs_grad(b) else None]
+    elif op == OP["MUL"]:
+        back = lambda g: [AG.reduce_to(g * b, a.getShape()) if AG.needs_grad(a) else None,  # noqa: E731
+                          AG.reduce_to(g * a, b.getShape()) if AG.needs_grad(b) else None]
+    elif op == OP["DIV"]:
+        back = lambda g: [AG.reduce_to(g / b, a.getShape()) if AG.needs_grad(a) else None,  # noqa: E731
+                          AG.reduce_to(-(g * a) / (b * b), b.getShape()) if AG.needs_grad(b) else None]
+    elif op in (OP["GT"], OP["LT"], OP["EQ"], OP["NE"], OP["GE"], OP["LE"]):
+        return  # comparisons carry no gradient
+    else:
+        raise InvalidArgumentException("Backward is not implemented for this binary operation")
+    AG.record(out, [a, b], back, "binary")
+
+
+def _record_scalar(out, a, s, op, reverse):
+    if op == OP["ADD"]:
+        back = lambda g: [g]  # noqa: E731
+    elif op == OP["SUB"]:
+        back = (lambda g: [-g]) if reverse else (lambda g: [g])  # noqa: E731
+    elif op == OP["MUL"]:
+        back = lambda g: [g * s]  # noqa: E731
+    elif op == OP["DIV"]:
+        back = (lambda g: [-(g * s) / (a * a)]) if reverse else (lambda g: [g / s])  # noqa: E731
+    elif op in (OP["GT"], OP["LT"], OP["EQ"], OP["NE"], OP["GE"], OP["LE"]):
+        return
+    else:
+        raise InvalidArgumentException("Backward is not implemented for this scalar operation")
+    AG.record(out, [a], back, "scalar")
+
+
+def _record_reduce(out, a, axis, op):
+    shape = a.getShape()
+    ax = None if axis is None else axis % len(shape)
+    if op == OP["SUM"]:
+        back = lambda g: [AG.expand_reduced(g, shape, ax)]  # noqa: E731
+    elif op == OP["MEAN"]:
+        n = a.getSize() if ax is None else shape[ax]
+        back = lambda g: [AG.expand_reduced(g / float(n), shape, ax)]  # noqa: E731
+    elif op in (OP["MAX"], OP["MIN"]):
+        def back(g):
+            # the upstream gradient is shared equally among the extrema
+            # (autograd.c:945-1003)
+            hit = a.eq(AG.expand_reduced(out, shape, ax)).astype(g.getDtype())
+            counts = hit.sum() if ax is None else hit.sum(ax)
+            share = AG.expand_reduced(g / counts, shape, ax)
+            return [CudaArray.where(hit, share, share * 0.0)]
+    else:
+        raise InvalidArgumentException("Backward is not implemented for this reduction")
+    AG.record(out, [a], back, "reduce")
