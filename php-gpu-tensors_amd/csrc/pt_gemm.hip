@@ -50,6 +50,9 @@ struct GemmArgs {
     long long bsa[GEMM_MAX_BATCH_DIMS];
     long long bsb[GEMM_MAX_BATCH_DIMS];
     int remap;             // total tiles divisible by 8: XCD remap on
+    int vec_a, vec_b;      // 16-byte aligned packs: the checked kernel loads in-range packs whole
+    int ksplit, k_chunk;   // split-K: blockIdx.y = K chunk of k_chunk (a multiple of BK)
+    float *partial;        // split-K fp32 partials [ksplit][batch][M][N]
 };
 
 // Element traits: storage type and elements per 16-byte pack.
@@ -141,7 +144,7 @@ struct TileLoader {
     // src(r, k) = base[r * s_r + k * s_k]; rows [r0, r0+R) of r_total,
     // k in [k0, k0+BK) of K.
     __device__ __forceinline__ void load(const S *base, long long s_r, long long s_k, int r0,
-                                         int r_total, int k0, int K, int tid)
+                                         int r_total, int k0, int K, int tid, int vec = 0)
     {
         if constexpr (KC) {
 #pragma unroll
@@ -149,7 +152,7 @@ struct TileLoader {
                 int p = tid + j * T;
                 int r = p / (BK / PK), kp = p % (BK / PK);
                 int gr = r0 + r, gk = k0 + kp * PK;
-                if constexpr (!CHECK) {
+                if (!CHECK || (vec && gr < r_total && gk + PK <= K)) {
                     kc[j] = *(const Pack *)(base + (long long)gr * s_r + gk);
                 } else {
                     Pack pk = {0u, 0u, 0u, 0u};
@@ -169,7 +172,7 @@ struct TileLoader {
 #pragma unroll
             for (int e = 0; e < PK; e++) {
                 int gk = k0 + kg * PK + e;
-                if constexpr (!CHECK) {
+                if (!CHECK || (vec && gk < K && gr + VR <= r_total)) {
                     const S *p = base + (long long)gk * s_k + gr;
                     if constexpr (VR * sizeof(S) == 16) {
                         uint4 v = *(const uint4 *)p;
@@ -295,8 +298,12 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 
     long long oa, ob;
     batch_offsets(g, bidx, oa, ob);
-    const S *A = (const S *)g.a + oa;
-    const S *B = (const S *)g.b + ob;
+    // split-K: this workgroup's K chunk [kbase, kbase + Kl)
+    const int split = blockIdx.y;
+    const int kbase = split * g.k_chunk;
+    const int Kl = g.ksplit > 1 ? min(g.k_chunk, g.K - kbase) : g.K;
+    const S *A = (const S *)g.a + oa + (long long)kbase * g.a_sk;
+    const S *B = (const S *)g.b + ob + (long long)kbase * g.b_sk;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -316,13 +323,13 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 #pragma unroll
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
-    const int KT = (g.K + BK - 1) / BK;
+    const int KT = (Kl + BK - 1) / BK;
     // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
-    la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, g.K, tid);
-    lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, g.K, tid);
+    la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, Kl, tid, g.vec_a);
+    lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, Kl, tid, g.vec_b);
     if (KT > 1) {
-        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, g.K, tid);
-        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, g.K, tid);
+        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, Kl, tid, g.vec_a);
+        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, Kl, tid, g.vec_b);
     }
     la[0].template store<LDK>(lds_a[0], tid);
     lb[0].template store<LDK>(lds_b[0], tid);
@@ -356,8 +363,8 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
                     TileLoader<DT, BN, BK, T, B_KC, CHECK> &lb_) {
         const int cur = kt & 1;
         if (kt + 2 < KT) {
-            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, g.K, tid);
-            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, g.K, tid);
+            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, Kl, tid, g.vec_a);
+            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, Kl, tid, g.vec_b);
         }
 #pragma unroll
         for (int sl = 0; sl < NS; sl++) {
@@ -393,7 +400,9 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 
     // ---- epilogue: lane holds column n = lane%32 and rows
     // 8*(e/4) + 4*(lane/32) + e%4 of each 32x32 block.
-    char *Cb = (char *)g.c + (size_t)bidx * (size_t)g.M * (size_t)g.N * sizeof(S);
+    const size_t mn = (size_t)g.M * (size_t)g.N;
+    char *Cb = (char *)g.c + (size_t)bidx * mn * sizeof(S);
+    float *Pb = g.ksplit > 1 ? g.partial + ((size_t)split * g.batch + bidx) * mn : nullptr;
     const int col_l = lane & 31;
     const int row_l = (lane >> 5) * 4;
 #pragma unroll
@@ -404,10 +413,25 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const int m = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
-                if (!CHECK || (m < g.M && n < g.N))
-                    store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
+                if (!CHECK || (m < g.M && n < g.N)) {
+                    if (Pb) Pb[(size_t)m * g.N + n] = acc[i][j][e];
+                    else store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
+                }
             }
         }
+}
+
+// Split-K epilogue: C = sum of the K-chunk partials, in chunk order, rounded
+// once to the output dtype.
+template <int DT>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partial, void *__restrict__ c,
+                                                       size_t count, int ksplit)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float acc = partial[i];
+    for (int k = 1; k < ksplit; k++) acc += partial[(size_t)k * count + i];
+    store_c<DT>(c, i, acc);
 }
 
 // ------------------------------------------- direct-to-LDS 16-bit kernel
@@ -598,33 +622,33 @@ static int g_sched = 2;
 template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
 static void launch_cfg(const GemmArgs &g, hipStream_t s)
 {
-    long long grid = (long long)g.tiles_m * g.tiles_n * g.batch;
+    const dim3 grid((unsigned)((long long)g.tiles_m * g.tiles_n * g.batch), (unsigned)(g.ksplit > 1 ? g.ksplit : 1));
     if constexpr (BM == 256 && BN == 128 && A_KC && !B_KC && !CHECK && DT != PT_FLOAT32) {
         // two workgroups per CU: waves sharing a SIMD belong to different
         // workgroups, so their barrier phases do not coincide
         if (g_sched >= 4) {
             if (g_sched == 4)
-                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 0, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 0, 2><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
             else
-                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+                k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2, 2><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
             return;
         }
     }
     if constexpr (BM == 256 && BN == 256 && A_KC && !B_KC && !CHECK && DT != PT_FLOAT32) {
         if (g_sched == 1) {
-            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 1><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 1><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
             return;
         }
         if (g_sched == 2) {
-            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 2><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
             return;
         }
         if (g_sched == 3) {
-            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 3><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+            k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 3><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
             return;
         }
     }
-    k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK><<<dim3((unsigned)grid), dim3(64 * WM * WN), 0, s>>>(g);
+    k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
 }
 
 template <int DT, int BM, int BN, int BK, int WM, int WN>
@@ -648,12 +672,12 @@ static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, 
 enum GemmTile {
     TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
-    TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_COUNT = 10
+    TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_COUNT = 11
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
     {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
-    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}};
+    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}};
 
 static int g_tile_override = -1;
 
@@ -688,6 +712,7 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
     // 8 waves on a 256x128 tile (128x32 per wave): the fp32 kernel that
     // keeps its accumulators and staging in registers without spilling
     case TILE_256x128_W8: launch_layouts<DT, 256, 128, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
+    case TILE_128x128_W8: launch_layouts<DT, 128, 128, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
     default: launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     }
 }
@@ -814,7 +839,8 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
                    ? (dtype == PT_FLOAT32 ? TILE_256x128_W8 : TILE_256x256_DIRECT)
-                   : (g.M >= 128 && g.N >= 128) ? TILE_128x128 : TILE_64x64;
+                   : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? TILE_128x128_W8 : TILE_128x128)
+                                                : TILE_64x64;
     }
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     if (tile == TILE_256x256_DIRECT) {
@@ -861,13 +887,66 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         for (int d = 0; d < g.nbd; d++)
             if (g.bsa[d] % PKe || g.bsb[d] % PKe) check = true;
     }
+    // checked kernels still load whole 16-byte packs that lie inside the
+    // matrix when the operand's contiguous stride is 1 and its pitch and
+    // batch offsets keep packs aligned
+    {
+        bool va = aligned(a) && (a_kc ? (g.a_sk == 1 && g.a_sm % PKe == 0) : (g.a_sm == 1 && g.a_sk % PKe == 0));
+        bool vb = aligned(b) && (b_kc ? (g.b_sk == 1 && g.b_sn % PKe == 0) : (g.b_sn == 1 && g.b_sk % PKe == 0));
+        for (int d = 0; d < g.nbd; d++) {
+            if (g.bsa[d] % PKe) va = false;
+            if (g.bsb[d] % PKe) vb = false;
+        }
+        g.vec_a = va;
+        g.vec_b = vb;
+    }
     long long total_tiles = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * batch;
     g.remap = total_tiles % 8 == 0;
     if (total_tiles > 0x7fffffffLL) return fail(PT_ERR_INVALID, "matmul grid too large");
+    // split-K when the tiles cannot fill the GPU and K is long: fp32
+    // partials per K chunk, then one ordered sum per output element
+    g.ksplit = 1;
+    g.k_chunk = g.K;
+    g.partial = nullptr;
+    if (total_tiles < 128 && g.K >= 8 * BK) {
+        long long want = (512 + total_tiles - 1) / total_tiles;
+        long long max_split = g.K / (4 * BK);
+        int ks = (int)(want < max_split ? want : max_split);
+        if (ks > 64) ks = 64;
+        if (ks > 1) {
+            int chunk = (g.K + ks - 1) / ks;
+            chunk = (chunk + BK - 1) / BK * BK;
+            ks = (g.K + chunk - 1) / chunk;
+            if (ks > 1) {
+                const size_t count = (size_t)batch * g.M * g.N;
+                PT_TRY(scratch_alloc((void **)&g.partial, sizeof(float) * count * (size_t)ks, s));
+                g.ksplit = ks;
+                g.k_chunk = chunk;
+            }
+        }
+    }
     switch (dtype) {
     case PT_BFLOAT16: launch_dt<PT_BFLOAT16>(g, tile, a_kc, b_kc, check, s); break;
     case PT_FLOAT16: launch_dt<PT_FLOAT16>(g, tile, a_kc, b_kc, check, s); break;
     default: launch_dt<PT_FLOAT32>(g, tile, a_kc, b_kc, check, s); break;
+    }
+    if (g.ksplit > 1) {
+        hipError_t e1 = hipGetLastError();
+        const size_t count = (size_t)batch * g.M * g.N;
+        const unsigned blocks = (unsigned)((count + 255) / 256);
+        switch (dtype) {
+        case PT_BFLOAT16: k_splitk_reduce<PT_BFLOAT16><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
+        case PT_FLOAT16: k_splitk_reduce<PT_FLOAT16><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
+        default: k_splitk_reduce<PT_FLOAT32><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
+        }
+        hipError_t e2 = hipGetLastError();
+        scratch_free(g.partial, s);
+        PT_TRY(check_hip(e1, "matmul (split-K partials)"));
+        PT_TRY(check_hip(e2, "matmul (split-K sum)"));
+        counters().mfma_gemm_calls++;
+        snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s",
+                 dtype == PT_FLOAT32 ? "mfma-fp32-splitk" : "mfma-low-precision-splitk");
+        return PT_OK;
     }
     PT_LAUNCH_CHECK("matmul");
     counters().mfma_gemm_calls++;

@@ -995,6 +995,49 @@ __global__ __launch_bounds__(256) void k_column_reduce(const void *__restrict__ 
     }
 }
 
+// Split column reduction for short outer / long middle axes: workgroup
+// (cx, split, o) reduces 64 columns over its contiguous slice of the middle
+// axis into partial[(o * splits + split) * inner + col]; the final pass
+// merges the slices of each column in order (index ties resolve to the
+// lowest index as in the single-pass kernel).
+__global__ __launch_bounds__(256) void k_column_partial(const void *__restrict__ x, int op, int dt,
+                                                        size_t n, size_t inner, size_t slice,
+                                                        GenAcc *__restrict__ partial)
+{
+    __shared__ GenAcc lds[4][64];
+    const int lx = threadIdx.x & 63, ly = threadIdx.x >> 6;
+    const size_t col = (size_t)blockIdx.x * 64 + lx;
+    const size_t split = blockIdx.y, o_outer = blockIdx.z;
+    GenAcc a;
+    gen_init(a, op, dt);
+    const size_t s_lo = split * slice;
+    const size_t s_hi = s_lo + slice < n ? s_lo + slice : n;
+    if (col < inner && s_lo < s_hi) {
+        size_t per = (s_hi - s_lo + 3) / 4;
+        size_t lo = s_lo + ly * per, hi = lo + per < s_hi ? lo + per : s_hi;
+        const size_t base = o_outer * n * inner + col;
+        for (size_t i = lo; i < hi; i++) gen_add(a, x, base + i * inner, (int)i);
+    }
+    lds[ly][lx] = a;
+    __syncthreads();
+    if (ly == 0 && col < inner) {
+        for (int k = 1; k < 4; k++) gen_merge(a, lds[k][lx]);
+        partial[(o_outer * gridDim.y + split) * inner + col] = a;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_column_final(const GenAcc *__restrict__ partial, size_t outer,
+                                                      size_t splits, size_t inner, void *__restrict__ out,
+                                                      GenParams p)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= outer * inner) return;
+    const size_t o = i / inner, col = i % inner;
+    GenAcc a = partial[(o * splits) * inner + col];
+    for (size_t k = 1; k < splits; k++) gen_merge(a, partial[(o * splits + k) * inner + col]);
+    gen_finish(a, p, out, i);
+}
+
 // Global reduction of a contiguous input: stage 1 writes one GenAcc per
 // workgroup (each takes a contiguous slice, so index ties resolve to the
 // lowest index), stage 2 merges them in order.
@@ -1251,6 +1294,28 @@ static pt_status reduce_driver(const void *input, void *output, int dtype, int r
         size_t outer = 1, inner = 1;
         for (int d = 0; d < axis; d++) outer *= (size_t)shape[d];
         for (int d = axis + 1; d < ndims; d++) inner *= (size_t)shape[d];
+        const size_t col_blocks = (inner + 63) / 64;
+        // too few workgroups for the GPU: split the reduced axis as well
+        if (outer <= 65535 && col_blocks * outer < 1024 && count >= 256) {
+            size_t splits = (2048 + col_blocks * outer - 1) / (col_blocks * outer);
+            const size_t max_splits = (count + 63) / 64;  // at least 64 rows per slice
+            if (splits > max_splits) splits = max_splits;
+            if (splits > 65535) splits = 65535;
+            const size_t slice = (count + splits - 1) / splits;
+            GenAcc *partial = nullptr;
+            PT_TRY(scratch_alloc((void **)&partial, sizeof(GenAcc) * outer * splits * inner, s));
+            k_column_partial<<<dim3((unsigned)col_blocks, (unsigned)splits, (unsigned)outer), 256, 0, s>>>(
+                xb, rop, dtype, count, inner, slice, partial);
+            hipError_t e1 = hipGetLastError();
+            k_column_final<<<(unsigned)((outer * inner + 255) / 256), 256, 0, s>>>(partial, outer, splits, inner,
+                                                                                  output, p);
+            hipError_t e2 = hipGetLastError();
+            scratch_free(partial, s);
+            PT_TRY(check_hip(e1, "column reduction (partials)"));
+            PT_TRY(check_hip(e2, "column reduction (final)"));
+            counters().column_reduce_calls++;
+            return PT_OK;
+        }
         if (outer <= 65535) {
             dim3 grid((unsigned)((inner + 63) / 64), (unsigned)outer);
             k_column_reduce<<<grid, 256, 0, s>>>(xb, output, rop, dtype,

@@ -72,7 +72,7 @@ def _ints(shape, seed, lo=-8, hi=8):
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9, 10])
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bmnk", SHAPES, ids=str)
 def test_matmul_integer_exact(A, bmnk, dt, tile):
@@ -83,6 +83,32 @@ def test_matmul_integer_exact(A, bmnk, dt, tile):
     a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
     got = run(A, a, b, dt)
     assert np.array_equal(got, ref(a, b, dt))
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
+@pytest.mark.parametrize("bmnk", [(1, 1024, 10, 4096), (1, 4096, 10, 1024), (3, 40, 24, 3000),
+                                  (1, 64, 64, 8192), (2, 65, 1, 257)], ids=str)
+def test_matmul_split_k(A, bmnk, dt):
+    """Few output tiles over a long K: the K range is split over workgroups
+    whose fp32 partials are summed in order and rounded once.  Integer inputs
+    keep every partial exact, so the result is bit-exact; random inputs stay
+    within the fp32 / low-precision bars of the module docstring."""
+    from phptensors import synthetic
+    b_, m, n, k = bmnk
+    a = O.to_storage(_ints((b_, m, k), seed=k + 3, lo=-3, hi=3), dt)
+    b = O.to_storage(_ints((b_, k, n), seed=k + 4, lo=-3, hi=3), dt)
+    assert np.array_equal(run(A, a, b, dt), ref(a, b, dt))
+    assert A.backend_info().last_matmul.decode().endswith("splitk")
+    a = O.to_storage(synthetic.normal((b_, m, k), 0.0, 1.0, seed=k + 5), dt)
+    b = O.to_storage(synthetic.normal((b_, k, n), 0.0, 1.0, seed=k + 6), dt)
+    got = O.from_storage(run(A, a, b, dt), dt).astype(np.float64)
+    r = O.from_storage(ref(a, b, dt), dt).astype(np.float64)
+    scale = np.abs(O.from_storage(a, dt).astype(np.float64)) @ np.abs(O.from_storage(b, dt).astype(np.float64))
+    if dt == O.F32:
+        tol = 1e-4 * math.sqrt(k) * scale
+    else:
+        tol = 1e-2 * np.maximum(np.abs(r), scale / math.sqrt(k))
+    assert np.all(np.abs(got - r) <= tol)
 
 
 @pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
