@@ -1038,6 +1038,121 @@ __global__ __launch_bounds__(256) void k_column_final(const GenAcc *__restrict__
     gen_finish(a, p, out, i);
 }
 
+// Typed column reductions (floating inputs; sum, mean, prod, max, min) of a
+// contiguous [outer, n, inner] input along n.  A 256-thread block owns
+// 64 * V adjacent columns; its four waves take interleaved rows of the
+// block's row slice (adjacent rows in flight together), each lane keeping V
+// columns in registers, and meet in LDS in wave order.  With one slice per
+// column the block writes the result; otherwise it writes a partial per
+// slice and k_col_final_t merges them in slice order.
+template <int DT, int OP, int V>
+__global__ __launch_bounds__(256) void k_col_reduce_t(const void *__restrict__ xin, size_t n, size_t inner,
+                                                      size_t slice, void *__restrict__ out, int out_dt,
+                                                      typename RT<DT>::C *__restrict__ partial)
+{
+    using S = typename RT<DT>::S;
+    using C = typename RT<DT>::C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t col = ((size_t)blockIdx.x * 64 + lane) * V;
+    const size_t split = blockIdx.y, o = blockIdx.z;
+    const size_t lo = split * slice;
+    const size_t hi = lo + slice < n ? lo + slice : n;
+    Acc<C, OP> acc[V];
+    if (col < inner) {
+        const S *x = (const S *)xin + o * n * inner + col;
+        size_t r = lo + wave;
+        for (; r + 12 < hi; r += 16) {
+            C v[4][V];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                if constexpr (V > 1) load_chunk<DT, V>(x + (r + 4 * u) * inner, v[u]);
+                else v[u][0] = RT<DT>::cv(x[(r + 4 * u) * inner]);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int k = 0; k < V; k++) acc[k].add(v[u][k], 0);
+        }
+        for (; r < hi; r += 4) {
+            C v[V];
+            if constexpr (V > 1) load_chunk<DT, V>(x + r * inner, v);
+            else v[0] = RT<DT>::cv(x[r * inner]);
+#pragma unroll
+            for (int k = 0; k < V; k++) acc[k].add(v[k], 0);
+        }
+    }
+    __shared__ C part[3][64 * V];
+    if (wave > 0)
+#pragma unroll
+        for (int k = 0; k < V; k++) part[wave - 1][lane * V + k] = acc[k].s;
+    __syncthreads();
+    if (wave != 0 || col >= inner) return;
+#pragma unroll
+    for (int w = 0; w < 3; w++)
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            Acc<C, OP> b;
+            b.s = part[w][lane * V + k];
+            acc[k].merge(b);
+        }
+#pragma unroll
+    for (int k = 0; k < V; k++) {
+        if (partial) {
+            partial[(o * gridDim.y + split) * inner + col + k] = acc[k].s;
+        } else {
+            C r = OP == R_MEAN ? acc[k].s / (C)n : acc[k].s;
+            store_out(out, out_dt, o * inner + col + k, r);
+        }
+    }
+}
+
+// Merge of the per-slice partials [outer][splits][inner]: wave w of a block
+// merges a contiguous quarter of the slices for 64 columns, then wave 0
+// merges the quarters in order.
+template <int DT, int OP>
+__global__ __launch_bounds__(256) void k_col_final_t(const typename RT<DT>::C *__restrict__ partial,
+                                                     size_t splits, size_t inner, size_t n,
+                                                     void *__restrict__ out, int out_dt)
+{
+    using C = typename RT<DT>::C;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t col = (size_t)blockIdx.x * 64 + lane, o = blockIdx.y;
+    const size_t q = (splits + 3) / 4;
+    const size_t lo = wave * q, hi = lo + q < splits ? lo + q : splits;
+    Acc<C, OP> acc;
+    if (col < inner) {
+        const C *p = partial + o * splits * inner + col;
+        size_t k = lo;
+        for (; k + 3 < hi; k += 4) {
+            C v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = p[(k + u) * inner];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                Acc<C, OP> b;
+                b.s = v[u];
+                acc.merge(b);
+            }
+        }
+        for (; k < hi; k++) {
+            Acc<C, OP> b;
+            b.s = p[k * inner];
+            acc.merge(b);
+        }
+    }
+    __shared__ C part[3][64];
+    if (wave > 0) part[wave - 1][lane] = acc.s;
+    __syncthreads();
+    if (wave != 0 || col >= inner) return;
+    for (int w = 0; w < 3; w++) {
+        Acc<C, OP> b;
+        b.s = part[w][lane];
+        acc.merge(b);
+    }
+    C r = OP == R_MEAN ? acc.s / (C)n : acc.s;
+    store_out(out, out_dt, o * inner + col, r);
+}
+
 // Global reduction of a contiguous input: stage 1 writes one GenAcc per
 // workgroup (each takes a contiguous slice, so index ties resolve to the
 // lowest index), stage 2 merges them in order.
@@ -1211,6 +1326,73 @@ static int result_dtype(int dtype, int rop)
     return dtype;
 }
 
+// Column launcher of k_col_reduce_t: whole-16-byte column packs when the
+// row pitch and base keep them aligned; when the column blocks cannot fill
+// the GPU the rows are split into slices (at least 64 rows each, at most
+// 128 slices) merged by k_col_final_t.
+template <int DT, int OP>
+static pt_status launch_cols_t(const void *x, size_t outer, size_t n, size_t inner, void *out, int out_dt,
+                               hipStream_t s)
+{
+    using C = typename RT<DT>::C;
+    constexpr int V = RT<DT>::V;
+    const bool vec = inner % V == 0 && aligned16(x);
+    const size_t cols_per_block = vec ? 64 * V : 64;
+    const size_t col_blocks = (inner + cols_per_block - 1) / cols_per_block;
+    size_t splits = 1;
+    if (col_blocks * outer < 1024) {
+        splits = (2048 + col_blocks * outer - 1) / (col_blocks * outer);
+        size_t max_splits = n / 64;
+        if (splits > max_splits) splits = max_splits;
+        if (splits > 128) splits = 128;
+        if (splits < 1) splits = 1;
+    }
+    const size_t slice = (n + splits - 1) / splits;
+    splits = (n + slice - 1) / slice;
+    C *partial = nullptr;
+    if (splits > 1) PT_TRY(scratch_alloc((void **)&partial, sizeof(C) * outer * splits * inner, s));
+    dim3 grid((unsigned)col_blocks, (unsigned)splits, (unsigned)outer);
+    if (vec) k_col_reduce_t<DT, OP, V><<<grid, 256, 0, s>>>(x, n, inner, slice, out, out_dt, partial);
+    else k_col_reduce_t<DT, OP, 1><<<grid, 256, 0, s>>>(x, n, inner, slice, out, out_dt, partial);
+    hipError_t e1 = hipGetLastError(), e2 = hipSuccess;
+    if (splits > 1) {
+        k_col_final_t<DT, OP><<<dim3((unsigned)((inner + 63) / 64), (unsigned)outer), 256, 0, s>>>(
+            partial, splits, inner, n, out, out_dt);
+        e2 = hipGetLastError();
+        scratch_free(partial, s);
+    }
+    PT_TRY(check_hip(e1, "column reduction"));
+    PT_TRY(check_hip(e2, "column reduction (merge)"));
+    return PT_OK;
+}
+
+template <int DT>
+static int launch_cols_dt(int rop, const void *x, size_t outer, size_t n, size_t inner, void *out, int out_dt,
+                          hipStream_t s)
+{
+    switch (rop) {
+    case R_SUM: return launch_cols_t<DT, R_SUM>(x, outer, n, inner, out, out_dt, s);
+    case R_MEAN: return launch_cols_t<DT, R_MEAN>(x, outer, n, inner, out, out_dt, s);
+    case R_PROD: return launch_cols_t<DT, R_PROD>(x, outer, n, inner, out, out_dt, s);
+    case R_MAX: return launch_cols_t<DT, R_MAX>(x, outer, n, inner, out, out_dt, s);
+    case R_MIN: return launch_cols_t<DT, R_MIN>(x, outer, n, inner, out, out_dt, s);
+    }
+    return -1;
+}
+
+// Returns -1 when the typed column path does not cover (dtype, op).
+static int launch_cols(int dt, int rop, const void *x, size_t outer, size_t n, size_t inner, void *out,
+                       int out_dt, hipStream_t s)
+{
+    switch (dt) {
+    case PT_FLOAT32: return launch_cols_dt<PT_FLOAT32>(rop, x, outer, n, inner, out, out_dt, s);
+    case PT_FLOAT64: return launch_cols_dt<PT_FLOAT64>(rop, x, outer, n, inner, out, out_dt, s);
+    case PT_BFLOAT16: return launch_cols_dt<PT_BFLOAT16>(rop, x, outer, n, inner, out, out_dt, s);
+    case PT_FLOAT16: return launch_cols_dt<PT_FLOAT16>(rop, x, outer, n, inner, out, out_dt, s);
+    }
+    return -1;
+}
+
 // Shared driver of pt_reduce / pt_arg_reduce / pt_moments.
 static pt_status reduce_driver(const void *input, void *output, int dtype, int rop, int out_dt,
                                const int *shape, const size_t *strides, int ndims, int axis,
@@ -1294,6 +1476,14 @@ static pt_status reduce_driver(const void *input, void *output, int dtype, int r
         size_t outer = 1, inner = 1;
         for (int d = 0; d < axis; d++) outer *= (size_t)shape[d];
         for (int d = axis + 1; d < ndims; d++) inner *= (size_t)shape[d];
+        if (outer <= 65535 && count <= (size_t)INT32_MAX) {
+            int st = launch_cols(dtype, rop, xb, outer, count, inner, output, out_dt, s);
+            if (st >= 0) {
+                PT_TRY((pt_status)st);
+                counters().column_reduce_calls++;
+                return PT_OK;
+            }
+        }
         const size_t col_blocks = (inner + 63) / 64;
         // too few workgroups for the GPU: split the reduced axis as well
         if (outer <= 65535 && col_blocks * outer < 1024 && count >= 256) {

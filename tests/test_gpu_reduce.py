@@ -157,6 +157,49 @@ def test_reduce_non_last_axis_and_global(G, axis, op):
         assert np.array_equal(got.ravel(), ref.ravel())
 
 
+@pytest.mark.parametrize("dt", [O.F32, O.F64, O.BF16, O.F16], ids=["f32", "f64", "bf16", "f16"])
+@pytest.mark.parametrize("shape,axis", [((4096, 1024), 0), ((4096, 10), 0), ((3, 700, 36), 1),
+                                        ((2, 20000, 8), 1), ((1000, 3000), 0), ((64, 70000), 0),
+                                        ((5, 1, 40), 1)], ids=str)
+def test_column_reductions(G, dt, shape, axis):
+    """Reductions along a non-last axis of a contiguous input (bias
+    gradients of the MLP step are sums over axis 0): split and unsplit row
+    ranges, packed and scalar columns, outer > 1.  Integer-valued inputs keep
+    float sums exact, so sum/max/min are bit-exact and mean within 1 ulp."""
+    from phptensors import synthetic
+    x = np.round(synthetic.uniform(shape, -64.0, 64.0, seed=sum(shape))).astype(np.float32)
+    x[(0,) * len(shape)] = 100.0
+    xs = O.to_storage(x.astype(np.float64) if dt == O.F64 else x, dt)
+    for op in ("sum", "mean", "max", "min"):
+        got, rdt = G.reduce(xs, dt, op, axis)
+        ref, rrdt = O.reduce(xs, dt, op, axis)
+        assert rdt == rrdt, op
+        if op == "mean":
+            assert np.allclose(got, ref, rtol=2e-7 if dt != O.F64 else 1e-15, atol=0), op
+        else:
+            assert np.array_equal(got.ravel(), ref.ravel()), op
+
+
+@pytest.mark.parametrize("dt", [O.F32, O.BF16], ids=["f32", "bf16"])
+def test_column_nan_and_inf(G, dt):
+    from phptensors import synthetic
+    # NaN in a column: max/min/sum of that column follow the oracle
+    y = synthetic.uniform((2048, 64), -1.0, 1.0, seed=78)
+    y[100, 5] = np.nan
+    y[7, 9] = np.inf
+    ys = O.to_storage(y, dt)
+    for op in ("max", "min", "sum"):
+        got, _ = G.reduce(ys, dt, op, 0)
+        ref, _ = O.reduce(ys, dt, op, 0)
+        assert np.array_equal(np.isnan(got), np.isnan(ref)), op
+        assert np.array_equal(np.isinf(got), np.isinf(ref)), op
+        fin = np.isfinite(ref)
+        if op == "sum":
+            assert np.allclose(got[fin], ref[fin], rtol=1e-4, atol=1e-4), op
+        else:
+            assert np.array_equal(got[fin], ref[fin]), op
+
+
 def test_reduce_transposed_view(G):
     from phptensors import synthetic
     base = synthetic.normal((40, 70), 0.0, 1.0, seed=301)
