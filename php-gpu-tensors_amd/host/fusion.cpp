@@ -216,13 +216,40 @@ static int collect(Plan &p, const TensorP &t, std::map<const Tensor *, int> &ind
     } else if (me.kind == IT_NATIVE) {
         me.cut = true;
         me.reason = "native";
-        for (int a : me.args)
-            if (p.items[a].kind == IT_ELEM) {
-                p.items[a].cut = true;
-                if (!p.items[a].reason) p.items[a].reason = "native-input";
+        for (int a : me.args) {
+            if (p.items[a].kind != IT_ELEM) continue;
+            // a chain of views over a value reaches the native step as a
+            // strided view of that value (no copy): only its base is
+            // materialized
+            int b = a;
+            while (p.items[b].kind == IT_ELEM && !p.items[b].cut && p.items[b].t->node->kind == N_VIEW)
+                b = p.items[b].args[0];
+            if (p.items[b].kind == IT_ELEM && !p.items[b].cut) {
+                p.items[b].cut = true;
+                p.items[b].reason = "native-input";
             }
+        }
     }
     return id;
+}
+
+// Steps that item `id` reads directly: cut elementwise items and native
+// items reached through uncut elementwise items (not past another step).
+static void direct_deps(const Plan &p, int id, std::vector<int> &out)
+{
+    std::vector<char> seen(p.items.size(), 0);
+    std::function<void(int)> walk = [&](int x) {
+        if (seen[x]) return;
+        seen[x] = 1;
+        const Item &it = p.items[x];
+        if (it.kind == IT_NATIVE || (it.kind == IT_ELEM && it.cut)) {
+            out.push_back(x);
+            return;
+        }
+        if (it.kind != IT_ELEM) return;
+        for (int a : it.args) walk(a);
+    };
+    for (int a : p.items[id].args) walk(a);
 }
 
 // ------------------------------------------------------------ leaf maps
@@ -762,53 +789,82 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
     }
     for (int id : p->outputs)
         if (p->items[id].kind == IT_ELEM) p->items[id].cut = true;
-    // steps in item (topological) order; elementwise roots with the same
-    // shape that do not depend on each other share one kernel
-    Kernel cur;
-    auto depends = [&](int id, const std::vector<int> &set) {
-        std::function<bool(int)> walk = [&](int x) -> bool {
-            if (std::find(set.begin(), set.end(), x) != set.end()) return true;
-            const Item &it = p->items[x];
-            if (it.kind != IT_ELEM) return false;
-            for (int a : it.args)
-                if (walk(a)) return true;
-            return false;
-        };
-        for (int a : p->items[id].args)
-            if (walk(a)) return true;
-        return false;
+    // Schedule by levels (as soon as possible).  A native step runs one
+    // level after the kernels it reads (at the level of natives it reads);
+    // a materialized elementwise root runs one level after kernel roots of
+    // another shape that it reads, at the level of natives it reads, and at
+    // the level of same-shape roots it reads, which it then evaluates
+    // inline in the same kernel (the vector kernel evaluates each node once
+    // per element; the general kernel's node functions recompute, so inline
+    // chains are at most kMaxInline deep).  Each level runs its natives in
+    // item order, then one kernel per shape (at most kMaxRoots roots each).
+    constexpr size_t kMaxRoots = 8;
+    constexpr int kMaxInline = 2;
+    const int nitems = (int)p->items.size();
+    std::vector<int> level(nitems, -1), depth(nitems, 0);
+    auto same_shape = [&](int a, int b) {
+        const Tensor &x = *p->items[a].t, &y = *p->items[b].t;
+        return x.ndims == y.ndims && std::equal(x.shape, x.shape + x.ndims, y.shape);
     };
-    auto flush = [&]() {
-        if (cur.roots.empty()) return;
-        cur.name = "fk" + std::to_string(p->kernels.size());
-        Step st;
-        st.kernel = (int)p->kernels.size();
-        p->kernels.push_back(cur);
-        p->steps.push_back(st);
-        cur = Kernel();
-    };
-    for (int id = 0; id < (int)p->items.size(); id++) {
+    int max_level = 0;
+    for (int id = 0; id < nitems; id++) {
         Item &it = p->items[id];
-        if (it.kind == IT_NATIVE) {
-            flush();
-            Step st;
-            st.native = true;
-            st.item = id;
-            p->steps.push_back(st);
-        } else if (it.kind == IT_ELEM && it.cut) {
-            const Tensor &t = *it.t;
-            bool same = !cur.roots.empty() && cur.ndims == t.ndims &&
-                        std::equal(t.shape, t.shape + t.ndims, cur.shape) && cur.roots.size() < 4;
-            if (!same || depends(id, cur.roots)) flush();
-            if (cur.roots.empty()) {
-                cur.ndims = t.ndims;
-                for (int d = 0; d < t.ndims; d++) cur.shape[d] = t.shape[d];
-                cur.total = t.numel();
+        if (it.kind != IT_NATIVE && !(it.kind == IT_ELEM && it.cut)) continue;
+        std::vector<int> deps;
+        direct_deps(*p, id, deps);
+        int L = 0;
+        for (int d : deps) {
+            bool dn = p->items[d].kind == IT_NATIVE;
+            bool in_line = it.kind == IT_ELEM && !dn && same_shape(d, id);
+            L = std::max(L, level[d] + (dn || in_line ? 0 : 1));
+        }
+        int dp = 0;
+        if (it.kind == IT_ELEM)
+            for (int d : deps)
+                if (p->items[d].kind == IT_ELEM && level[d] == L && same_shape(d, id))
+                    dp = std::max(dp, depth[d] + 1);
+        if (dp > kMaxInline) {
+            L++;
+            dp = 0;
+        }
+        level[id] = L;
+        depth[id] = dp;
+        max_level = std::max(max_level, L);
+    }
+    for (int L = 0; L <= max_level; L++) {
+        for (int id = 0; id < nitems; id++)
+            if (level[id] == L && p->items[id].kind == IT_NATIVE) {
+                Step st;
+                st.native = true;
+                st.item = id;
+                p->steps.push_back(st);
             }
-            cur.roots.push_back(id);
+        std::vector<Kernel> ks;
+        for (int id = 0; id < nitems; id++) {
+            if (level[id] != L || p->items[id].kind != IT_ELEM) continue;
+            const Tensor &t = *p->items[id].t;
+            Kernel *k = nullptr;
+            for (Kernel &c : ks)
+                if (c.ndims == t.ndims && std::equal(t.shape, t.shape + t.ndims, c.shape) &&
+                    c.roots.size() < kMaxRoots)
+                    k = &c;
+            if (!k) {
+                ks.emplace_back();
+                k = &ks.back();
+                k->ndims = t.ndims;
+                for (int d = 0; d < t.ndims; d++) k->shape[d] = t.shape[d];
+                k->total = t.numel();
+            }
+            k->roots.push_back(id);
+        }
+        for (Kernel &k : ks) {
+            k.name = "fk" + std::to_string(p->kernels.size());
+            Step st;
+            st.kernel = (int)p->kernels.size();
+            p->kernels.push_back(k);
+            p->steps.push_back(st);
         }
     }
-    flush();
     // leaves, maps and source
     std::ostringstream os;
     emit_prelude(os);
@@ -927,13 +983,37 @@ static bool launch_kernel(Plan &p, Kernel &k, std::vector<TensorP> &vals)
                         "Fusion kernel launch failed");
 }
 
+// Operand of a native step: a materialized value, or an uncut chain of
+// views over one, passed as a strided view of the value's storage.
+static TensorP native_arg(const Plan &p, std::vector<TensorP> &vals, int id)
+{
+    const Item &it = p.items[id];
+    if (it.kind != IT_ELEM || it.cut || it.t->node->kind != N_VIEW) return vals[id];
+    TensorP src = native_arg(p, vals, it.args[0]);
+    if (!src) return nullptr;
+    if (!src->contiguous()) src = materialize(src);
+    if (!src) return nullptr;
+    const FusionNode &n = *it.t->node;
+    TensorP v = make_meta(it.t->shape, it.t->ndims, it.t->dtype);
+    if (!v) return nullptr;
+    v->storage = src->storage;
+    v->offset = src->offset + n.view_offset;
+    for (int d = 0; d < v->ndims; d++) v->strides[d] = n.view_strides[d];
+    v->read_only = true;
+    return v;
+}
+
 static bool run_steps(Plan &p, std::vector<TensorP> &vals)
 {
     for (Step &st : p.steps) {
         if (st.native) {
             Item &it = p.items[st.item];
             std::vector<TensorP> ins;
-            for (int a : it.args) ins.push_back(vals[a]);
+            for (int a : it.args) {
+                TensorP v = native_arg(p, vals, a);
+                if (!v) return false;
+                ins.push_back(v);
+            }
             TensorP out = native_execute(it.t->node->native, ins);
             if (!out) return false;
             vals[st.item] = out;
