@@ -318,6 +318,19 @@ pt_status pt_module_unload(pt_module_t module);
 pt_status pt_launch(pt_function_t function, unsigned grid_x, unsigned block_x,
                     void **params, pt_stream_t stream);
 
+/* Scratch workspace of the calling thread.  Replaces the per-stream
+ * reduction workspaces that natives captured into a graph use
+ * (src/backends/cuda/reduction_ops.cu:11-60, released with the capture
+ * stream at fusion_plan.c:198-204).  Between begin and end, the scratch of
+ * multi-kernel operations (split-K partials, column and global reduction
+ * partials) is carved from [base, base + bytes) instead of the stream-
+ * ordered pool, so a captured graph holds no allocation; an operation whose
+ * scratch does not fit fails with PT_ERR_NOMEM.  base NULL and bytes 0:
+ * measuring mode (pool allocations, peak recorded).  end reports the peak
+ * scratch bytes held at once (256-byte granules). */
+pt_status pt_workspace_begin(void *base, size_t bytes);
+pt_status pt_workspace_end(size_t *peak_bytes);
+
 /* --------------------------------------------------------------- graphs --
  * Replaces the cuGraphCreate / cuGraphAddKernelNode / Instantiate /
  * ExecKernelNodeSetParams / cuGraphLaunch sequence of fusion_execute.c:

@@ -7,6 +7,7 @@
 
 #include <hip/hiprtc.h>
 
+#include <algorithm>
 #include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
@@ -94,14 +95,59 @@ hipStream_t stream_of(pt_stream_t s)
     return s ? (hipStream_t)s : g_stream;
 }
 
+// Scratch of the multi-kernel operations (split-K partials, column and
+// global reduction partials).  By default it comes from the stream-ordered
+// pool.  Between pt_workspace_begin and pt_workspace_end it is carved from
+// a caller-owned arena instead (a stack: each operation frees what it took
+// before it returns), so that a captured HIP graph holds no allocation; in
+// measuring mode (no arena) it still comes from the pool and the peak is
+// recorded, which sizes the arena.
+struct Workspace {
+    bool active = false, measure = false;
+    char *base = nullptr;
+    size_t bytes = 0, top = 0, peak = 0;
+    std::vector<std::pair<void *, size_t>> stack;
+};
+static thread_local Workspace t_ws;
+
+static size_t ws_round(size_t n) { return (n + 255) & ~(size_t)255; }
+
 pt_status scratch_alloc(void **ptr, size_t bytes, hipStream_t stream)
 {
-    return check_hip(hipMallocAsync(ptr, bytes ? bytes : 1, stream), "scratch allocation");
+    if (!t_ws.active) return check_hip(hipMallocAsync(ptr, bytes ? bytes : 1, stream), "scratch allocation");
+    const size_t need = ws_round(bytes ? bytes : 1);
+    if (t_ws.measure) {
+        PT_TRY(check_hip(hipMallocAsync(ptr, need, stream), "scratch allocation"));
+    } else {
+        if (t_ws.top + need > t_ws.bytes)
+            return fail(PT_ERR_NOMEM, "workspace of %zu bytes cannot hold %zu more scratch bytes", t_ws.bytes, need);
+        *ptr = t_ws.base + t_ws.top;
+    }
+    t_ws.top += need;
+    if (t_ws.top > t_ws.peak) t_ws.peak = t_ws.top;
+    t_ws.stack.push_back({*ptr, need});
+    return PT_OK;
 }
 
 void scratch_free(void *ptr, hipStream_t stream)
 {
-    if (ptr) (void)hipFreeAsync(ptr, stream);
+    if (!ptr) return;
+    if (!t_ws.active) {
+        (void)hipFreeAsync(ptr, stream);
+        return;
+    }
+    for (size_t i = t_ws.stack.size(); i-- > 0;) {
+        if (t_ws.stack[i].first != ptr) continue;
+        if (t_ws.measure) (void)hipFreeAsync(ptr, stream);
+        t_ws.stack.erase(t_ws.stack.begin() + (long)i);
+        // held bytes: the end of the highest live entry in the arena, the
+        // sum of the live entries when measuring
+        t_ws.top = 0;
+        for (auto &e : t_ws.stack)
+            t_ws.top = t_ws.measure ? t_ws.top + e.second
+                                    : std::max(t_ws.top, (size_t)((char *)e.first - t_ws.base) + e.second);
+        return;
+    }
 }
 
 }  // namespace pt
@@ -453,6 +499,29 @@ struct GraphHandle {
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
+
+pt_status pt_workspace_begin(void *base, size_t bytes)
+{
+    if (t_ws.active) return fail(PT_ERR_INVALID, "a workspace is already active on this thread");
+    if ((base == nullptr) != (bytes == 0)) return fail(PT_ERR_INVALID, "workspace needs a base and a size");
+    if (((uintptr_t)base & 255) != 0) return fail(PT_ERR_INVALID, "workspace base must be 256-byte aligned");
+    t_ws = Workspace();
+    t_ws.active = true;
+    t_ws.measure = base == nullptr;
+    t_ws.base = (char *)base;
+    t_ws.bytes = bytes;
+    return PT_OK;
+}
+
+pt_status pt_workspace_end(size_t *peak_bytes)
+{
+    if (!t_ws.active) return fail(PT_ERR_INVALID, "no workspace is active on this thread");
+    if (peak_bytes) *peak_bytes = t_ws.peak;
+    const bool leaked = !t_ws.stack.empty();
+    t_ws = Workspace();
+    if (leaked) return fail(PT_ERR_RUNTIME, "scratch still held at the end of the workspace");
+    return PT_OK;
+}
 
 pt_status pt_graph_begin_capture(pt_stream_t stream)
 {

@@ -168,6 +168,11 @@ struct Plan {
     bool pending = false;
     pt_event_t done = nullptr;
     std::vector<TensorP> pending_values;
+    // scratch arena of the native steps inside the captured graph, sized by
+    // the first (eager, measuring) run
+    bool workspace_sized = false;
+    size_t workspace_bytes = 0;
+    std::shared_ptr<Storage> workspace;
 };
 
 static bool is_elementwise(const FusionNode &n)
@@ -1014,7 +1019,9 @@ static bool run_steps(Plan &p, std::vector<TensorP> &vals)
                 if (!v) return false;
                 ins.push_back(v);
             }
+            preset_output(vals[st.item]);
             TensorP out = native_execute(it.t->node->native, ins);
+            preset_output(nullptr);
             if (!out) return false;
             vals[st.item] = out;
         } else {
@@ -1024,18 +1031,78 @@ static bool run_steps(Plan &p, std::vector<TensorP> &vals)
     return true;
 }
 
-// Allocate materialized values for a run (outside graph capture).
+// Allocate materialized values for a run (outside graph capture): kernel
+// roots and the outputs of native steps.
 static bool prepare_values(Plan &p, std::vector<TensorP> &vals)
 {
+    auto give = [&](int id) {
+        const Tensor &t = *p.items[id].t;
+        auto st = buffer_for(p, id, t.numel() * dtype_size(t.dtype));
+        if (!st) return false;
+        TensorP v = make_meta(t.shape, t.ndims, t.dtype);
+        if (!v) return false;
+        v->storage = st;
+        vals[id] = v;
+        return true;
+    };
     for (Kernel &k : p.kernels)
-        for (int r : k.roots) {
-            const Tensor &t = *p.items[r].t;
-            auto st = buffer_for(p, r, t.numel() * dtype_size(t.dtype));
-            if (!st) return false;
-            TensorP v = make_meta(t.shape, t.ndims, t.dtype);
-            v->storage = st;
-            vals[r] = v;
-        }
+        for (int r : k.roots)
+            if (!give(r)) return false;
+    for (Step &st : p.steps)
+        if (st.native && !give(st.item)) return false;
+    return true;
+}
+
+// First run of a graph plan with native steps: eager, with the natives'
+// scratch measured to size the workspace the captured graph will use.
+static bool measuring_run(Plan &p, std::vector<TensorP> &vals)
+{
+    if (!check_status(pt_workspace_begin(nullptr, 0), "Workspace setup failed")) return false;
+    bool ok = run_steps(p, vals);
+    size_t peak = 0;
+    pt_status st = pt_workspace_end(&peak);
+    if (!ok) return false;
+    if (!check_status(st, "Workspace measurement failed")) return false;
+    // at least one granule, so that the arena always has a base
+    const size_t bytes = peak > 256 ? peak : 256;
+    auto ws = std::make_shared<Storage>();
+    ws->bytes = bytes;
+    if (!check_status(pt_alloc(&ws->ptr, bytes, nullptr), "Fusion workspace allocation")) return false;
+    p.workspace = ws;
+    p.tensor_allocations++;
+    p.workspace_bytes = bytes;
+    p.workspace_sized = true;
+    return true;
+}
+
+// Record the steps into `p.graph`.  Native steps run with the workspace as
+// their scratch and must not allocate; when they cannot (a native that
+// needs a temporary copy, scratch beyond the measured peak) the capture is
+// dropped, the plan keeps to eager execution and `captured` is false.
+static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, bool &captured)
+{
+    captured = false;
+    if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
+    bool ok = true;
+    if (natives)
+        ok = check_status(pt_workspace_begin(p.workspace->ptr, p.workspace_bytes), "Workspace setup failed");
+    if (ok) {
+        allocation_forbidden() = natives;
+        ok = run_steps(p, vals);
+        allocation_forbidden() = false;
+        if (natives && !check_status(pt_workspace_end(nullptr), "Workspace release failed")) ok = false;
+    }
+    if (!ok) {
+        pt_graph_t scrap = nullptr;
+        if (pt_graph_end_capture(nullptr, &scrap) == PT_OK && scrap) pt_graph_destroy(scrap);
+        p.graph_compatible = false;
+        p.incompatibility = "a native step allocates during capture";
+        clear_error();
+        return true;
+    }
+    pt_status st = p.graph ? pt_graph_end_capture_update(nullptr, p.graph) : pt_graph_end_capture(nullptr, &p.graph);
+    if (!check_status(st, "Graph instantiation failed")) return false;
+    captured = true;
     return true;
 }
 
@@ -1057,28 +1124,30 @@ static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<Ten
     bool graph_ok = p.use_graph && p.graph_compatible;
     bool native_present = false;
     for (Step &st : p.steps) native_present = native_present || st.native;
-    if (graph_ok && native_present) {
-        // native steps allocate their results; pre-run once eagerly so that
-        // their buffers come from the pool, then replay the whole plan from
-        // the graph only when every step is an elementwise kernel
-        graph_ok = false;
+    bool ran = false;
+    if (graph_ok && native_present && !p.workspace_sized) {
+        if (!measuring_run(p, vals)) return false;
+        ran = true;
     }
-    if (graph_ok) {
+    if (graph_ok && !ran) {
         std::vector<void *> ptrs;
         for (size_t i = 0; i < vals.size(); i++)
             if (vals[i]) ptrs.push_back(vals[i]->data());
         if (!p.graph || ptrs != p.graph_ptrs) {
-            if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
-            bool ok = run_steps(p, vals);
-            pt_status st = p.graph ? pt_graph_end_capture_update(nullptr, p.graph)
-                                   : pt_graph_end_capture(nullptr, &p.graph);
-            if (!ok) return false;
-            if (!check_status(st, "Graph instantiation failed")) return false;
-            p.graph_ptrs = ptrs;
+            bool captured = false;
+            if (!capture_steps(p, vals, native_present, captured)) return false;
+            if (captured) {
+                p.graph_ptrs = ptrs;
+            } else {
+                if (!run_steps(p, vals)) return false;
+                ran = true;
+            }
         }
-        if (!check_status(pt_graph_launch(p.graph, nullptr), "Graph launch failed")) return false;
-        p.graph_launches++;
-    } else {
+        if (!ran) {
+            if (!check_status(pt_graph_launch(p.graph, nullptr), "Graph launch failed")) return false;
+            p.graph_launches++;
+        }
+    } else if (!ran) {
         if (!run_steps(p, vals)) return false;
     }
     if (wait) {

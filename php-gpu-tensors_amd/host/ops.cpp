@@ -242,7 +242,7 @@ TensorP cuda_tensor_reduce(const TensorP &a, int axis, int op)
         return fusion_record_native(sp, {a}, shape, nd, rdt);
     }
     if (!guard(a)) return nullptr;
-    TensorP out = make_empty(shape, nd, rdt);
+    TensorP out = output_tensor(shape, nd, rdt);
     if (!out) return nullptr;
     if (!check_status(pt_reduce(base_ptr(a), out->storage->ptr, a->dtype, op, a->shape, a->strides,
                                 a->ndims, axis == kGlobalAxis ? -1 : axis, a->offset, nullptr),
@@ -268,7 +268,7 @@ TensorP cuda_tensor_reduce_arg(const TensorP &a, int axis, int op)
         return fusion_record_native(sp, {a}, shape, nd, PT_INT32);
     }
     if (!guard(a)) return nullptr;
-    TensorP out = make_empty(shape, nd, PT_INT32);
+    TensorP out = output_tensor(shape, nd, PT_INT32);
     if (!out) return nullptr;
     if (!check_status(pt_arg_reduce(base_ptr(a), (int32_t *)out->storage->ptr, a->dtype, op, a->shape,
                                     a->strides, a->ndims, axis == kGlobalAxis ? -1 : axis, a->offset,
@@ -304,7 +304,7 @@ TensorP cuda_array_variance(const TensorP &a, int axis, long correction, bool st
         src = materialize(a);
         if (!src) return nullptr;
     }
-    TensorP out = make_empty(shape, nd, rdt);
+    TensorP out = output_tensor(shape, nd, rdt);
     if (!out) return nullptr;
     if (!check_status(pt_moments(base_ptr(src), out->storage->ptr, src->dtype, rdt, src->shape,
                                  src->strides, src->ndims, axis == kGlobalAxis ? -1 : axis,
@@ -339,7 +339,7 @@ TensorP cuda_array_softmax(const TensorP &a, int axis)
         src = materialize(src);
         if (!src) return nullptr;
     }
-    TensorP out = make_empty(a->shape, a->ndims, odt);
+    TensorP out = output_tensor(a->shape, a->ndims, odt);
     if (!out) return nullptr;
     if (!check_status(pt_softmax(base_ptr(src), out->storage->ptr, src->dtype, odt, src->shape,
                                  src->strides, src->ndims, axis, nullptr),
@@ -467,7 +467,7 @@ TensorP cuda_array_layernorm(const TensorP &a, const int *axes_in, int naxes, do
 
     int pshape[kMaxDims];
     for (int d = 0; d < a->ndims; d++) pshape[d] = a->shape[perm[d]];
-    TensorP outp = make_empty(pshape, a->ndims, cdt);
+    TensorP outp = identity ? output_tensor(pshape, a->ndims, cdt) : make_empty(pshape, a->ndims, cdt);
     if (!outp) return nullptr;
     if (rows && !check_status(pt_layernorm(xp->data(), outp->storage->ptr, xp->dtype, cdt, rows, n, eps,
                                            g ? g->data() : nullptr, b ? b->data() : nullptr, nullptr),
@@ -504,7 +504,7 @@ TensorP cuda_tensor_matmul(const TensorP &a, const TensorP &b)
         return fusion_record_native(sp, {a, b}, shape, nd, a->dtype);
     }
     if (!guard(a) || !guard(b)) return nullptr;
-    TensorP out = make_empty(shape, nd, a->dtype);
+    TensorP out = output_tensor(shape, nd, a->dtype);
     if (!out) return nullptr;
     const char *pa = (const char *)base_ptr(a) + a->offset * dtype_size(a->dtype);
     const char *pb = (const char *)base_ptr(b) + b->offset * dtype_size(b->dtype);

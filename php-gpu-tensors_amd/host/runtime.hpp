@@ -105,6 +105,14 @@ bool to_host(const TensorP &t, void *out, size_t bytes);     // logical row-majo
 TensorP full(const int *shape, int ndims, int dtype, const Scalar &value);
 TensorP materialize(const TensorP &t);                       // contiguous copy if needed
 
+// Native steps of a plan captured into a HIP graph must not allocate: while
+// allocation_forbidden() is set, make_empty fails.  A plan hands a native
+// step its (stable) output buffer with preset_output; the native operation
+// takes it through output_tensor when shape and dtype match.
+bool &allocation_forbidden();
+void preset_output(const TensorP &t);
+TensorP output_tensor(const int *shape, int ndims, int dtype);
+
 // views (share storage)
 TensorP view(const TensorP &t, const int *shape, const size_t *strides, int ndims, size_t offset);
 TensorP reshape(const TensorP &t, const int *shape, int ndims);

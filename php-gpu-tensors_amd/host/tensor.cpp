@@ -4,6 +4,8 @@
 // copies go through the C-ABI (pt_alloc / pt_memcpy_* / pt_cast).
 #include "runtime.hpp"
 
+#include <algorithm>
+
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -449,8 +451,29 @@ TensorP make_meta(const int *shape, int ndims, int dtype)
     return t;
 }
 
+static thread_local bool t_alloc_forbidden = false;
+static thread_local TensorP t_preset;
+
+bool &allocation_forbidden() { return t_alloc_forbidden; }
+
+void preset_output(const TensorP &t) { t_preset = t; }
+
+TensorP output_tensor(const int *shape, int ndims, int dtype)
+{
+    TensorP p = std::move(t_preset);
+    t_preset.reset();
+    if (p && p->storage && p->dtype == dtype && p->ndims == ndims && std::equal(shape, shape + ndims, p->shape) &&
+        p->contiguous() && p->storage->bytes >= p->numel() * dtype_size(dtype))
+        return p;
+    return make_empty(shape, ndims, dtype);
+}
+
 TensorP make_empty(const int *shape, int ndims, int dtype)
 {
+    if (t_alloc_forbidden) {
+        set_runtime("Device allocation inside a captured plan");
+        return nullptr;
+    }
     TensorP t = make_meta(shape, ndims, dtype);
     if (!t) return nullptr;
     auto st = std::make_shared<Storage>();

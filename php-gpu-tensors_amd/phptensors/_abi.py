@@ -141,6 +141,8 @@ SIGNATURES = {
     "pt_graph_launch": (ctypes.c_int, [vp, vp]),
     "pt_graph_destroy": (ctypes.c_int, [vp]),
     "pt_graph_node_count": (ctypes.c_int, [vp, c_size_p]),
+    "pt_workspace_begin": (ctypes.c_int, [vp, ctypes.c_size_t]),
+    "pt_workspace_end": (ctypes.c_int, [c_size_p]),
 }
 
 

@@ -147,8 +147,34 @@ def test_compiled_training_step_matches_eager_and_replays():
     assert losses[-1] < losses[0]
     st = graph.getStats()
     assert st["executions"] == 5
+    # the first run sizes the natives' workspace eagerly; later runs capture
+    # the whole plan (natives included) into a HIP graph
+    assert st["cudaGraphCompatible"] == 1
+    assert st["graphLaunches"] == 4
     kinds = [s["kind"] for s in graph.getPlan()]
     assert kinds.count("native") >= 9  # forward + backward GEMMs and reductions
+
+
+def test_compiled_step_graph_replays_match_eager():
+    """Replays of the captured step (natives inside the graph, scratch in
+    the plan's workspace) give the eager step's results on every replay."""
+    layers, rows = (784, 1024, 1024, 10), 512
+    params, xt, yt, x, y = make(rows, layers, 11)
+    opt = Optimizer.adamW()
+    state = opt.initState(params)
+    rate = CudaArray.full([1], 1e-3)
+    eager = mlp.train_batch(xt, yt, params, opt, state, rate)
+    inputs = mlp.training_inputs(xt, yt, rate, params, state)
+    graph = mlp.compile_training_plan(inputs, opt)
+    for rep in range(3):
+        graph.replay(2, *inputs)
+        p1, s1, loss1 = mlp.unpack_step(graph.run(*inputs))
+        np.testing.assert_allclose(loss1.toNumpy(), eager["loss"].toNumpy(), rtol=1e-6)
+        for a, b in zip(p1, eager["parameters"]):
+            np.testing.assert_allclose(a.toNumpy(), b.toNumpy(), rtol=1e-6, atol=1e-7)
+        for a, b in zip(s1["firstMoment"], eager["state"]["firstMoment"]):
+            np.testing.assert_allclose(a.toNumpy(), b.toNumpy(), rtol=1e-5, atol=1e-10)
+    assert graph.getStats()["graphLaunches"] >= 6
 
 
 def test_config5_full_size_step():
