@@ -41,6 +41,9 @@ void phpt_shape(phpt_tensor *t, int *shape);
 void phpt_strides(phpt_tensor *t, size_t *strides);
 size_t phpt_size(phpt_tensor *t);
 int phpt_is_lazy(phpt_tensor *t);
+/* 1 for a tensor made by a view operation (slice, transpose, reshape,
+ * broadcast, select): __serialize refuses those (cuda_array_ce.c:276-280) */
+int phpt_is_view(phpt_tensor *t);
 int phpt_dtype_from_name(const char *name);
 const char *phpt_dtype_name(int dtype);
 

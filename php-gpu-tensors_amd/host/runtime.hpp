@@ -81,6 +81,7 @@ struct Tensor {
     size_t strides[kMaxDims] = {0};  // elements
     size_t offset = 0;               // elements
     bool read_only = false;          // broadcast views
+    bool is_view = false;            // made by a view operation (shares storage)
     std::shared_ptr<FusionNode> node;  // set while recorded in a Fusion scope
     uint64_t id = 0;
 

@@ -541,6 +541,7 @@ TensorP view(const TensorP &t, const int *shape, const size_t *strides, int ndim
     }
     v->offset = offset;
     v->read_only = t->read_only;
+    v->is_view = true;
     v->id = next_tensor_id();
     return v;
 }

@@ -28,6 +28,7 @@ SIGNATURES = {
     "phpt_strides": (None, [T, sp]),
     "phpt_size": (ctypes.c_size_t, [T]),
     "phpt_is_lazy": (ctypes.c_int, [T]),
+    "phpt_is_view": (ctypes.c_int, [T]),
     "phpt_dtype_from_name": (ctypes.c_int, [ctypes.c_char_p]),
     "phpt_dtype_name": (ctypes.c_char_p, [ctypes.c_int]),
     "phpt_reshape": (T, [T, ip, ctypes.c_int]),

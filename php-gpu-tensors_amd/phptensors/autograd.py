@@ -93,8 +93,6 @@ def backward(root, gradient=None):
     visit(root)
     if gradient is None:
         gradient = CudaArray.ones(root.getShape(), root.getDtype())
-    elif gradient.getShape() != root.getShape():
-        gradient = gradient.broadcastTo(root.getShape())
     grads = {id(root): gradient}
     _recording[0] = False  # gradients carry no history of their own
     try:

@@ -59,7 +59,8 @@ def bf16_bits_to_f32(bits):
 
 def f32_to_bf16_bits(x):
     """Round-to-nearest-even float32 -> bfloat16 bit pattern (data_types.c:96-131)."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    x = np.asarray(x, dtype=np.float32)
+    u = np.ascontiguousarray(x).view(np.uint32).reshape(x.shape)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     lsb = (u >> 16) & 1
     r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
@@ -500,8 +501,19 @@ class CudaArray:
         return self
 
     def backward(self, gradient=None, retainGraph=False):
+        """autograd_backward (autograd.c:1710-1735): argument checks, then
+        the reverse walk."""
         if not AG.needs_grad(self):
-            raise RuntimeException("backward() on a tensor that does not require gradients")
+            raise InvalidArgumentException("backward() requires a tensor marked with requiresGrad()")
+        if self.getDtype() not in ("float32", "float64", "float16", "bfloat16"):
+            raise InvalidArgumentException(
+                "backward() is only supported for float32, float64, float16 and bfloat16 tensors")
+        if gradient is None and self.getSize() != 1:
+            raise InvalidArgumentException(
+                "A gradient seed is required when backward() is called on a non-scalar tensor")
+        if gradient is not None and (gradient.getShape() != self.getShape()
+                                     or gradient.getDtype() != self.getDtype()):
+            raise InvalidArgumentException("The backward gradient seed must match the tensor shape and dtype")
         AG.backward(self, gradient)
         if not retainGraph:
             self._node = None
@@ -521,7 +533,10 @@ class CudaArray:
 
 
 def _from_bits(arr, code):
-    arr = np.ascontiguousarray(arr)
+    # np.ascontiguousarray would turn a rank-0 array into shape (1,)
+    arr = np.asarray(arr)
+    if not arr.flags.c_contiguous:
+        arr = arr.copy(order="C")
     sh, n = _ints(arr.shape)
     return _host.load().phpt_from_host(arr.ctypes.data_as(ctypes.c_void_p), code, sh, n)
 
@@ -593,3 +608,81 @@ def _record_reduce(out, a, axis, op):
     else:
         raise InvalidArgumentException("Backward is not implemented for this reduction")
     AG.record(out, [a], back, "reduce")
+
+
+# ------------------------------------------------------------ serialization
+# CudaArray::__serialize / __unserialize (cuda_array_ce.c:270-366): a
+# versioned payload of metadata and the raw row-major element bytes.  The
+# validation of a payload restates tensor_import_serialized_shape
+# (tensor_import.c:90-123) and the size checks of :337-352; a payload that
+# fails any check raises InvalidArgumentException and leaves the target
+# unchanged.  Snapshots carry values only, never gradients or history.
+_SERIAL_VERSION = "__cuda_array_v1"
+_MAX_DIMS = 10
+_LONG_MAX = 2 ** 63 - 1
+_INT_MAX = 2 ** 31 - 1
+
+
+def _is_long(v):
+    return isinstance(v, int) and not isinstance(v, bool)
+
+
+def _serialize(self):
+    lib = _host.load()
+    if lib.phpt_is_view(self._h):
+        raise RuntimeException("Cannot serialize non-contiguous CudaArray views")
+    code = lib.phpt_dtype(self._h)
+    return {_SERIAL_VERSION: "1", "ndims": self.getNdims(), "dtype": DTYPE_NAMES[code],
+            "total_elements": self.getSize(), "element_size": np.dtype(BITS_OF[code]).itemsize,
+            "shape": self.getShape(), "data": self.toBuffer()}
+
+
+def _payload_tensor(data):
+    if not isinstance(data, dict):
+        raise InvalidArgumentException("Invalid serialized CudaArray payload")
+    version = data.get(_SERIAL_VERSION)
+    if not isinstance(version, str) or version != "1":
+        raise InvalidArgumentException("Invalid serialized CudaArray payload")
+    nd, dt, shape = data.get("ndims"), data.get("dtype"), data.get("shape")
+    raw, total, esize = data.get("data"), data.get("total_elements"), data.get("element_size")
+    if (not _is_long(nd) or not isinstance(dt, str) or not isinstance(shape, (list, tuple))
+            or not isinstance(raw, (bytes, bytearray)) or not _is_long(total) or not _is_long(esize)):
+        raise InvalidArgumentException("Malformed serialized CudaArray payload")
+    if "\0" in dt or dt not in DTYPES:
+        raise InvalidArgumentException(f"Invalid serialized CudaArray dtype: {dt.split(chr(0))[0]}")
+    code = DTYPES[dt]
+    if nd < 0 or nd > _MAX_DIMS or len(shape) != nd:
+        raise InvalidArgumentException("Invalid serialized tensor shape")
+    for d in shape:
+        if not _is_long(d) or d < 0 or d > _INT_MAX:
+            raise InvalidArgumentException("Invalid serialized tensor dimension")
+    elements = 1
+    for d in reversed(shape):
+        if elements > _LONG_MAX or (d and elements > _LONG_MAX // d):
+            raise InvalidArgumentException("Serialized tensor shape or strides exceed supported limits")
+        elements *= d
+    width = np.dtype(BITS_OF[code]).itemsize
+    if total < 0 or total != elements or esize != width:
+        raise InvalidArgumentException("Invalid serialized CudaArray size metadata")
+    if len(raw) != elements * width:
+        raise InvalidArgumentException(
+            f"Serialized CudaArray data size mismatch: expected {elements * width} bytes, got {len(raw)}")
+    return CudaArray.fromBuffer(bytes(raw), list(shape), dt)
+
+
+def _unserialize(self, data):
+    fresh = _payload_tensor(data)
+    old = self._h
+    self._h, fresh._h = fresh._h, old
+    self._rg = False
+    self._node = None
+    self._grad = None
+
+
+def _reduce(self):
+    return (_payload_tensor, (_serialize(self),))
+
+
+setattr(CudaArray, "__serialize", _serialize)
+setattr(CudaArray, "__unserialize", _unserialize)
+CudaArray.__reduce__ = _reduce
