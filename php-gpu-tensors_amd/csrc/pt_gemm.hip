@@ -130,28 +130,58 @@ __device__ __forceinline__ S load_elem_checked(const S *p, long long off, bool o
 }
 
 // Stage one operand tile (R rows x BK k) from global memory into registers.
-// KC: k is the contiguous dimension of the source.
-template <int DT, int R, int BK, int T, bool KC, bool CHECK>
+// KC: k is the contiguous dimension of the source.  KM (r-contiguous
+// sources only): the tile goes to LDS k-major, [k][r], as 16-byte packs of
+// r loaded and stored whole; fragment reads then gather their k values.
+template <int DT, int R, int BK, int T, bool KC, bool CHECK, bool KM = false, bool CLAMP = false>
 struct TileLoader {
     using S = typename GE<DT>::S;
     static constexpr int PK = GE<DT>::PK;
-    static constexpr int P = R * BK / PK / T;         // packs per thread (KC)
+    static constexpr int P = R * BK / PK / T;         // packs per thread (KC, KM)
     static constexpr int VR = R * BK / (T * PK);      // r per thread (RC)
     static constexpr int DW = (VR * (int)sizeof(S) + 3) / 4;  // dwords per RC row load
-    Pack kc[KC ? P : 1];
-    uint32_t rc[KC ? 1 : PK][KC ? 1 : (DW > 0 ? DW : 1)];
+    static_assert(!KM || (!KC && P >= 1 && (R / PK) * BK % T == 0), "k-major staging");
+    // CLAMP (unchecked loads on an edge tile): rows past r_total read the
+    // last whole row or pack instead; they only feed outputs that are not
+    // stored
+    static_assert(!CLAMP || (!CHECK && (KC || KM)), "clamped staging");
+    Pack kc[(KC || KM) ? P : 1];
+    uint32_t rc[(KC || KM) ? 1 : PK][(KC || KM) ? 1 : (DW > 0 ? DW : 1)];
 
     // src(r, k) = base[r * s_r + k * s_k]; rows [r0, r0+R) of r_total,
     // k in [k0, k0+BK) of K.
     __device__ __forceinline__ void load(const S *base, long long s_r, long long s_k, int r0,
                                          int r_total, int k0, int K, int tid, int vec = 0)
     {
-        if constexpr (KC) {
+        if constexpr (KM) {
+            // pack p: k row p / (R / PK), r pack p % (R / PK); a wave reads
+            // whole rows of r
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                int p = tid + j * T;
+                int k = p / (R / PK), rp = p % (R / PK);
+                int gr = r0 + rp * PK, gk = k0 + k;
+                if constexpr (CLAMP) gr = min(gr, r_total - PK);
+                if (!CHECK || (vec && gk < K && gr + PK <= r_total)) {
+                    kc[j] = *(const Pack *)(base + (long long)gk * s_k + gr);
+                } else {
+                    Pack pk = {0u, 0u, 0u, 0u};
+#pragma unroll
+                    for (int e = 0; e < PK; e++) {
+                        S v = load_elem_checked(base, (long long)gk * s_k + (long long)(gr + e) * s_r,
+                                                gk < K && gr + e < r_total);
+                        pk[e * sizeof(S) / 4] |= to_bits(v) << (8 * ((e * sizeof(S)) % 4));
+                    }
+                    kc[j] = pk;
+                }
+            }
+        } else if constexpr (KC) {
 #pragma unroll
             for (int j = 0; j < P; j++) {
                 int p = tid + j * T;
                 int r = p / (BK / PK), kp = p % (BK / PK);
                 int gr = r0 + r, gk = k0 + kp * PK;
+                if constexpr (CLAMP) gr = min(gr, r_total - 1);
                 if (!CHECK || (vec && gr < r_total && gk + PK <= K)) {
                     kc[j] = *(const Pack *)(base + (long long)gr * s_r + gk);
                 } else {
@@ -199,11 +229,19 @@ struct TileLoader {
         }
     }
 
-    // Write the staged tile to LDS laid out [r][k] with row pitch LDK.
+    // Write the staged tile to LDS laid out [r][k] with row pitch LDK (or,
+    // KM, [k][r] with row pitch LDK).
     template <int LDK>
     __device__ __forceinline__ void store(S *lds, int tid)
     {
-        if constexpr (KC) {
+        if constexpr (KM) {
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                int p = tid + j * T;
+                int k = p / (R / PK), rp = p % (R / PK);
+                *(Pack *)(lds + k * LDK + rp * PK) = kc[j];
+            }
+        } else if constexpr (KC) {
 #pragma unroll
             for (int j = 0; j < P; j++) {
                 int p = tid + j * T;
@@ -266,17 +304,172 @@ __device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long lon
     }
 }
 
+// LDS layout of one stage.  fp32 operands whose r is contiguous in memory
+// stay k-major in LDS ([k][r], row pitch r + 8: the two half-waves of a
+// fragment read, four k rows apart, fall on different banks); the others
+// are [r][k] with the row padded by one pack.
+template <int DT, int BM, int BN, int BK, bool A_KC, bool B_KC>
+struct GemmLds {
+    static constexpr int PK = GE<DT>::PK;
+    static constexpr int LDK = BK + PK;
+    static constexpr bool AKM = DT == PT_FLOAT32 && !A_KC;
+    static constexpr bool BKM = DT == PT_FLOAT32 && !B_KC;
+    static constexpr int LDA = AKM ? BM + 8 : LDK, LDB = BKM ? BN + 8 : LDK;
+    static constexpr int SA = AKM ? BK * LDA : BM * LDK;
+    static constexpr int SB = BKM ? BK * LDB : BN * LDK;
+};
+
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK, int SCHED,
+          bool CLAMP = false>
+__device__ __forceinline__ void gemm_core(const GemmArgs &g,
+                                          typename GE<DT>::S (&lds_a)[2][GemmLds<DT, BM, BN, BK, A_KC, B_KC>::SA],
+                                          typename GE<DT>::S (&lds_b)[2][GemmLds<DT, BM, BN, BK, A_KC, B_KC>::SB],
+                                          const typename GE<DT>::S *A, const typename GE<DT>::S *B, int Kl,
+                                          int bidx, int split, int m0, int n0)
+{
+    using C = GemmCfg<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK>;
+    using S = typename C::S;
+    using L = GemmLds<DT, BM, BN, BK, A_KC, B_KC>;
+    constexpr int T = C::T, PK = C::PK, LDK = C::LDK, TM = C::TM, TN = C::TN;
+    constexpr bool AKM = L::AKM, BKM = L::BKM;
+    constexpr int LDA = L::LDA, LDB = L::LDB;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+
+    // Two register staging sets: the global loads of tile k+2 are issued
+    // while tile k runs on the matrix cores and tile k+1 waits in the other
+    // set, giving the loads two K steps of MFMA work to arrive.
+    using LoaderA = TileLoader<DT, BM, BK, T, A_KC, CHECK, AKM, CLAMP>;
+    using LoaderB = TileLoader<DT, BN, BK, T, B_KC, CHECK, BKM, CLAMP>;
+    LoaderA la[2];
+    LoaderB lb[2];
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+    const int KT = (Kl + BK - 1) / BK;
+    // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
+    la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, Kl, tid, g.vec_a);
+    lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, Kl, tid, g.vec_b);
+    if (KT > 1) {
+        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, Kl, tid, g.vec_a);
+        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, Kl, tid, g.vec_b);
+    }
+    la[0].template store<LDA>(lds_a[0], tid);
+    lb[0].template store<LDB>(lds_b[0], tid);
+    __syncthreads();
+
+    const int arow = wm * C::WTM + (lane & 31);
+    const int brow = wn * C::WTN + (lane & 31);
+    const int khalf = (lane >> 5) * PK;
+    // One k-slice feeds one MFMA per (i, j) block: 16 k for 16-bit operands,
+    // 8 k (four 32x32x2 MFMAs) for fp32.  Fragments of slice s+1 are read
+    // from LDS into the second register set while slice s runs on the
+    // matrix cores, so LDS latency overlaps MFMA execution.
+    constexpr int KS = 2 * PK;
+    constexpr int NS = BK / KS;
+    using Frag = typename FragT<DT>::type;
+    Frag fa[2][TM], fb[2][TN];
+    auto read_frags = [&](const S *sa, const S *sb, int slice, Frag (&ra)[TM], Frag (&rb)[TN]) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            if constexpr (AKM) {
+#pragma unroll
+                for (int e = 0; e < PK; e++) ra[i][e] = sa[(slice * KS + khalf + e) * LDA + arow + i * 32];
+            } else {
+                ra[i] = *(const Frag *)(sa + (arow + i * 32) * LDK + slice * KS + khalf);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            if constexpr (BKM) {
+#pragma unroll
+                for (int e = 0; e < PK; e++) rb[j][e] = sb[(slice * KS + khalf + e) * LDB + brow + j * 32];
+            } else {
+                rb[j] = *(const Frag *)(sb + (brow + j * 32) * LDK + slice * KS + khalf);
+            }
+        }
+    };
+    read_frags(lds_a[0], lds_b[0], 0, fa[0], fb[0]);
+
+    // step kt: W holds tile kt+1 (to LDS after the MFMAs), L receives tile kt+2
+    auto step = [&](int kt, LoaderA &wa, LoaderB &wb, LoaderA &la_, LoaderB &lb_) {
+        const int cur = kt & 1;
+        if (kt + 2 < KT) {
+            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, Kl, tid, g.vec_a);
+            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, Kl, tid, g.vec_b);
+        }
+#pragma unroll
+        for (int sl = 0; sl < NS; sl++) {
+            if (sl + 1 < NS)
+                read_frags(lds_a[cur], lds_b[cur], sl + 1, fa[(sl + 1) & 1], fb[(sl + 1) & 1]);
+            mfma_block<DT, TM, TN>(acc, fa[sl & 1], fb[sl & 1]);
+            if constexpr (SCHED == 1) {
+                __builtin_amdgcn_iglp_opt(0);
+            } else if constexpr (SCHED == 2) {
+                __builtin_amdgcn_iglp_opt(1);
+            } else if constexpr (SCHED == 3) {
+                // interleave: one MFMA, then one LDS read, for the reads of
+                // the next slice; remaining MFMAs follow
+#pragma unroll
+                for (int q = 0; q < TM + TN; q++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
+            }
+        }
+        if (kt + 1 < KT) {
+            wa.template store<LDA>(lds_a[cur ^ 1], tid);
+            wb.template store<LDB>(lds_b[cur ^ 1], tid);
+        }
+        __syncthreads();
+        if (kt + 1 < KT) read_frags(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, fa[0], fb[0]);
+    };
+    for (int kt = 0; kt < KT; kt += 2) {
+        step(kt, la[1], lb[1], la[0], lb[0]);
+        if (kt + 1 < KT) step(kt + 1, la[0], lb[0], la[1], lb[1]);
+    }
+
+    // ---- epilogue: lane holds column n = lane%32 and rows
+    // 8*(e/4) + 4*(lane/32) + e%4 of each 32x32 block.
+    const size_t mn = (size_t)g.M * (size_t)g.N;
+    char *Cb = (char *)g.c + (size_t)bidx * mn * sizeof(S);
+    float *Pb = g.ksplit > 1 ? g.partial + ((size_t)split * g.batch + bidx) * mn : nullptr;
+    const int col_l = lane & 31;
+    const int row_l = (lane >> 5) * 4;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + wn * C::WTN + j * 32 + col_l;
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const int m = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
+                if ((!CHECK && !CLAMP) || (m < g.M && n < g.N)) {
+                    if (Pb) Pb[(size_t)m * g.N + n] = acc[i][j][e];
+                    else store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
+                }
+            }
+        }
+}
+
 template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK,
           int SCHED = 0, int MINW = 1>
 __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 {
-    using C = GemmCfg<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK>;
-    using S = typename C::S;
-    constexpr int T = C::T, PK = C::PK, LDK = C::LDK, TM = C::TM, TN = C::TN;
+    using S = typename GE<DT>::S;
     constexpr int GROUP_M = 4;
 
-    __shared__ __attribute__((aligned(16))) S lds_a[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) S lds_b[2][BN * LDK];
+    using L = GemmLds<DT, BM, BN, BK, A_KC, B_KC>;
+    __shared__ __attribute__((aligned(16))) S lds_a[2][L::SA];
+    __shared__ __attribute__((aligned(16))) S lds_b[2][L::SB];
 
     // ---- tile selection (XCD-aware remap + grouped ordering)
     const int ntile = g.tiles_m * g.tiles_n;
@@ -305,121 +498,28 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
     const S *A = (const S *)g.a + oa + (long long)kbase * g.a_sk;
     const S *B = (const S *)g.b + ob + (long long)kbase * g.b_sk;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
-
-    // Two register staging sets: the global loads of tile k+2 are issued
-    // while tile k runs on the matrix cores and tile k+1 waits in the other
-    // set, giving the loads two K steps of MFMA work to arrive.
-    TileLoader<DT, BM, BK, T, A_KC, CHECK> la[2];
-    TileLoader<DT, BN, BK, T, B_KC, CHECK> lb[2];
-
-    floatx16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-
-    const int KT = (Kl + BK - 1) / BK;
-    // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
-    la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, Kl, tid, g.vec_a);
-    lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, Kl, tid, g.vec_b);
-    if (KT > 1) {
-        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, Kl, tid, g.vec_a);
-        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, Kl, tid, g.vec_b);
+    if constexpr (CHECK) {
+        // Whole K steps and packable operands: tiles wholly inside M x N run
+        // the unchecked core, edge tiles the same core with clamped rows and
+        // a guarded store (all of one launch's workgroups run at once, so an
+        // edge tile as slow as a checked one would set the launch's time);
+        // only ragged K or unpackable operands pay for per-element checks.
+        constexpr bool CLAMPABLE = (A_KC || L::AKM) && (B_KC || L::BKM);
+        const bool whole = g.vec_a && g.vec_b && Kl % BK == 0;
+        const bool interior = whole && m0 + BM <= g.M && n0 + BN <= g.N;
+        const bool clampable = whole && (A_KC || g.M % GE<DT>::PK == 0) && (B_KC || g.N % GE<DT>::PK == 0);
+        if (interior)
+            gemm_core<DT, BM, BN, BK, WM, WN, A_KC, B_KC, false, SCHED>(g, lds_a, lds_b, A, B, Kl, bidx, split, m0, n0);
+        else if (CLAMPABLE && clampable)
+            gemm_core<DT, BM, BN, BK, WM, WN, A_KC, B_KC, false, SCHED, CLAMPABLE>(g, lds_a, lds_b, A, B, Kl, bidx,
+                                                                                split, m0, n0);
+        else
+            gemm_core<DT, BM, BN, BK, WM, WN, A_KC, B_KC, true, SCHED>(g, lds_a, lds_b, A, B, Kl, bidx, split, m0, n0);
+    } else {
+        gemm_core<DT, BM, BN, BK, WM, WN, A_KC, B_KC, false, SCHED>(g, lds_a, lds_b, A, B, Kl, bidx, split, m0, n0);
     }
-    la[0].template store<LDK>(lds_a[0], tid);
-    lb[0].template store<LDK>(lds_b[0], tid);
-    __syncthreads();
-
-    const int arow = wm * C::WTM + (lane & 31);
-    const int brow = wn * C::WTN + (lane & 31);
-    const int khalf = (lane >> 5) * PK;
-    // One k-slice feeds one MFMA per (i, j) block: 16 k for 16-bit operands,
-    // 8 k (four 32x32x2 MFMAs) for fp32.  Fragments of slice s+1 are read
-    // from LDS into the second register set while slice s runs on the
-    // matrix cores, so LDS latency overlaps MFMA execution.
-    constexpr int KS = 2 * PK;
-    constexpr int NS = BK / KS;
-    using Frag = typename FragT<DT>::type;
-    Frag fa[2][TM], fb[2][TN];
-    auto read_frags = [&](const S *sa, const S *sb, int slice, Frag (&ra)[TM], Frag (&rb)[TN]) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-            ra[i] = *(const Frag *)(sa + (arow + i * 32) * LDK + slice * KS + khalf);
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-            rb[j] = *(const Frag *)(sb + (brow + j * 32) * LDK + slice * KS + khalf);
-    };
-    read_frags(lds_a[0], lds_b[0], 0, fa[0], fb[0]);
-
-    // step kt: W holds tile kt+1 (to LDS after the MFMAs), L receives tile kt+2
-    auto step = [&](int kt, TileLoader<DT, BM, BK, T, A_KC, CHECK> &wa,
-                    TileLoader<DT, BN, BK, T, B_KC, CHECK> &wb,
-                    TileLoader<DT, BM, BK, T, A_KC, CHECK> &la_,
-                    TileLoader<DT, BN, BK, T, B_KC, CHECK> &lb_) {
-        const int cur = kt & 1;
-        if (kt + 2 < KT) {
-            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, Kl, tid, g.vec_a);
-            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, Kl, tid, g.vec_b);
-        }
-#pragma unroll
-        for (int sl = 0; sl < NS; sl++) {
-            if (sl + 1 < NS)
-                read_frags(lds_a[cur], lds_b[cur], sl + 1, fa[(sl + 1) & 1], fb[(sl + 1) & 1]);
-            mfma_block<DT, TM, TN>(acc, fa[sl & 1], fb[sl & 1]);
-            if constexpr (SCHED == 1) {
-                __builtin_amdgcn_iglp_opt(0);
-            } else if constexpr (SCHED == 2) {
-                __builtin_amdgcn_iglp_opt(1);
-            } else if constexpr (SCHED == 3) {
-                // interleave: one MFMA, then one LDS read, for the reads of
-                // the next slice; remaining MFMAs follow
-#pragma unroll
-                for (int q = 0; q < TM + TN; q++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-                }
-                __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
-            }
-        }
-        if (kt + 1 < KT) {
-            wa.template store<LDK>(lds_a[cur ^ 1], tid);
-            wb.template store<LDK>(lds_b[cur ^ 1], tid);
-        }
-        __syncthreads();
-        if (kt + 1 < KT) read_frags(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, fa[0], fb[0]);
-    };
-    for (int kt = 0; kt < KT; kt += 2) {
-        step(kt, la[1], lb[1], la[0], lb[0]);
-        if (kt + 1 < KT) step(kt + 1, la[0], lb[0], la[1], lb[1]);
-    }
-
-    // ---- epilogue: lane holds column n = lane%32 and rows
-    // 8*(e/4) + 4*(lane/32) + e%4 of each 32x32 block.
-    const size_t mn = (size_t)g.M * (size_t)g.N;
-    char *Cb = (char *)g.c + (size_t)bidx * mn * sizeof(S);
-    float *Pb = g.ksplit > 1 ? g.partial + ((size_t)split * g.batch + bidx) * mn : nullptr;
-    const int col_l = lane & 31;
-    const int row_l = (lane >> 5) * 4;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + wn * C::WTN + j * 32 + col_l;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const int m = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
-                if (!CHECK || (m < g.M && n < g.N)) {
-                    if (Pb) Pb[(size_t)m * g.N + n] = acc[i][j][e];
-                    else store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
-                }
-            }
-        }
 }
+
 
 // Split-K epilogue: C = sum of the K-chunk partials, in chunk order, rounded
 // once to the output dtype.
@@ -619,7 +719,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_direct(GemmArgs g)
 // ---------------------------------------------------------------- host side
 static int g_sched = 2;
 
-template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK>
+template <int DT, int BM, int BN, int BK, int WM, int WN, bool A_KC, bool B_KC, bool CHECK, int MINW = 1>
 static void launch_cfg(const GemmArgs &g, hipStream_t s)
 {
     const dim3 grid((unsigned)((long long)g.tiles_m * g.tiles_n * g.batch), (unsigned)(g.ksplit > 1 ? g.ksplit : 1));
@@ -648,22 +748,22 @@ static void launch_cfg(const GemmArgs &g, hipStream_t s)
             return;
         }
     }
-    k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
+    k_gemm<DT, BM, BN, BK, WM, WN, A_KC, B_KC, CHECK, 0, MINW><<<grid, dim3(64 * WM * WN), 0, s>>>(g);
 }
 
-template <int DT, int BM, int BN, int BK, int WM, int WN>
+template <int DT, int BM, int BN, int BK, int WM, int WN, int MINW = 1>
 static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, hipStream_t s)
 {
     if (check) {
-        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, true>(g, s);
-        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, true>(g, s);
-        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, true>(g, s);
-        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, true>(g, s);
+        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, true, MINW>(g, s);
+        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, true, MINW>(g, s);
+        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, true, MINW>(g, s);
+        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, true, MINW>(g, s);
     } else {
-        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, false>(g, s);
-        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, false>(g, s);
-        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, false>(g, s);
-        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, false>(g, s);
+        if (a_kc && b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, true, false, MINW>(g, s);
+        else if (a_kc) launch_cfg<DT, BM, BN, BK, WM, WN, true, false, false, MINW>(g, s);
+        else if (b_kc) launch_cfg<DT, BM, BN, BK, WM, WN, false, true, false, MINW>(g, s);
+        else launch_cfg<DT, BM, BN, BK, WM, WN, false, false, false, MINW>(g, s);
     }
 }
 
@@ -672,12 +772,14 @@ static void launch_layouts(const GemmArgs &g, bool a_kc, bool b_kc, bool check, 
 enum GemmTile {
     TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
-    TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_COUNT = 11
+    TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_128x128_W8_K2 = 11,
+    TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13, TILE_COUNT = 14
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
     {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
-    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}};
+    {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}, {128, 128, 2},
+    {128, 64, 1}, {128, 64, 2}};
 
 static int g_tile_override = -1;
 
@@ -713,6 +815,19 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
     // keeps its accumulators and staging in registers without spilling
     case TILE_256x128_W8: launch_layouts<DT, 256, 128, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
     case TILE_128x128_W8: launch_layouts<DT, 128, 128, BK, 2, 4>(g, a_kc, b_kc, check, s); break;
+    // fp32 only (the 16-bit types have their own kernels at these sizes)
+    case TILE_128x128_W8_K2:
+        if constexpr (DT == PT_FLOAT32) launch_layouts<DT, 128, 128, 2 * BK, 2, 4>(g, a_kc, b_kc, check, s);
+        break;
+    // 4 waves on 128x64 (64x32 per wave), two workgroups per CU: waves of
+    // different workgroups share each SIMD, so one fills the other's
+    // barrier and LDS-latency gaps
+    case TILE_128x64_W4M2:
+        if constexpr (DT == PT_FLOAT32) launch_layouts<DT, 128, 64, BK, 2, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
+    case TILE_128x64_W4M2_K2:
+        if constexpr (DT == PT_FLOAT32) launch_layouts<DT, 128, 64, 2 * BK, 2, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
     default: launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     }
 }
@@ -839,9 +954,12 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
                    ? (dtype == PT_FLOAT32 ? TILE_256x128_W8 : TILE_256x256_DIRECT)
-                   : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? TILE_128x128_W8 : TILE_128x128)
+                   : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? TILE_128x64_W4M2 : TILE_128x128)
                                                 : TILE_64x64;
     }
+    // the fp32-only tiles run the 128x128 kernel for 16-bit operands
+    if (dtype != PT_FLOAT32 && (tile == TILE_128x128_W8_K2 || tile == TILE_128x64_W4M2 || tile == TILE_128x64_W4M2_K2))
+        tile = TILE_128x128;
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     if (tile == TILE_256x256_DIRECT) {
         // direct-to-LDS kernel: 16-bit operands, whole 256x256 tiles, K a
@@ -903,13 +1021,15 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     long long total_tiles = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * batch;
     g.remap = total_tiles % 8 == 0;
     if (total_tiles > 0x7fffffffLL) return fail(PT_ERR_INVALID, "matmul grid too large");
-    // split-K when the tiles cannot fill the GPU and K is long: fp32
-    // partials per K chunk, then one ordered sum per output element
+    // split-K when the tiles cannot give every CU a workgroup and K is
+    // long: about 512 workgroups of K chunks (each at least 4 K steps)
+    // write fp32 partials, then one ordered sum per output element
     g.ksplit = 1;
     g.k_chunk = g.K;
     g.partial = nullptr;
-    if (total_tiles < 128 && g.K >= 8 * BK) {
-        long long want = (512 + total_tiles - 1) / total_tiles;
+    if (total_tiles < 256 && g.K >= 8 * BK) {
+        // whole rounds: about 2 workgroups per CU, never a partial second round
+        long long want = 512 / total_tiles;
         long long max_split = g.K / (4 * BK);
         int ks = (int)(want < max_split ? want : max_split);
         if (ks > 64) ks = 64;

@@ -64,7 +64,8 @@ def test_matmul_golden(A, case):
 
 
 SHAPES = [(1, 64, 64, 64), (2, 256, 128, 64), (3, 100, 70, 33), (1, 512, 256, 512),
-          (4, 128, 384, 96), (1, 1, 300, 5), (2, 65, 1, 257), (1, 33, 17, 1)]
+          (4, 128, 384, 96), (1, 1, 300, 5), (2, 65, 1, 257), (1, 33, 17, 1),
+          (1, 196, 100, 64), (2, 132, 260, 128)]
 
 
 def _ints(shape, seed, lo=-8, hi=8):
@@ -72,7 +73,7 @@ def _ints(shape, seed, lo=-8, hi=8):
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9, 10])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9, 10, 11, 12, 13])
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bmnk", SHAPES, ids=str)
 def test_matmul_integer_exact(A, bmnk, dt, tile):
@@ -156,9 +157,12 @@ def test_matmul_direct_lds_batch_broadcast(A):
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "TN", "NT", "TT"])
-def test_matmul_transposed_views(A, dt, layout):
-    """A and/or B passed as transposed strided views (no copy)."""
-    m, n, k = 96, 160, 72
+@pytest.mark.parametrize("mnk", [(96, 160, 72), (100, 132, 64), (196, 1024, 256)], ids=str)
+def test_matmul_transposed_views(A, dt, layout, mnk):
+    """A and/or B passed as transposed strided views (no copy).  Whole K
+    steps with ragged M/N run the edge tiles with clamped rows (the last two
+    shapes); a ragged K runs every tile checked (the first)."""
+    m, n, k = mnk
     a32 = _ints((m, k), seed=1)
     b32 = _ints((k, n), seed=2)
     a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
