@@ -568,11 +568,26 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
             }
         }
     }
+    // the next row's loads are issued before this row's reductions, so its
+    // HBM latency overlaps the barriers and stores of the current row (only
+    // while two rows and gamma/beta fit the register budget)
+    constexpr bool PF = NCH * VEC <= 32;
+    CT nx[NCH][VEC];
+    if constexpr (PF) load_row<DT, VEC, NCH, WPR, false>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, nx);
     for (; row < rows; row += row_step) {
-        const S *x = (const S *)xin + row * (size_t)n;
         CT *y = out + row * (size_t)n;
         CT v[NCH][VEC];
-        load_row<DT, VEC, NCH, WPR, false>(x, n, wr, lane, (CT)0, v);
+        if constexpr (PF) {
+#pragma unroll
+            for (int c = 0; c < NCH; c++)
+#pragma unroll
+                for (int k = 0; k < VEC; k++) v[c][k] = nx[c][k];
+            if (row + row_step < rows)
+                load_row<DT, VEC, NCH, WPR, false>((const S *)xin + (row + row_step) * (size_t)n, n, wr, lane,
+                                                   (CT)0, nx);
+        } else {
+            load_row<DT, VEC, NCH, WPR, false>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, v);
+        }
         CT s = 0;
 #pragma unroll
         for (int c = 0; c < NCH; c++)
