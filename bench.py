@@ -200,6 +200,45 @@ def fused_family(steps, warmup, replays=100):
             "stats": {k: stats[k] for k in ("fusedKernels", "graphLaunches", "cudaGraphCompatible")}}
 
 
+def eager_family(steps, warmup):
+    """Config 3 on the eager elementwise backend: m = y*z (row broadcast of
+    y), s = x + m, t = tanh(s), three launches through the C-ABI
+    (pt_broadcast, pt_broadcast, pt_unary), each timed against HBM."""
+    lib = A.load()
+    rows, n = 16384, 8192
+    x = A.to_device(synthetic.uniform((rows, n), -2.0, 2.0, seed=3))
+    z = A.to_device(synthetic.uniform((rows, n), -2.0, 2.0, seed=31))
+    y = A.to_device(synthetic.uniform((n,), -2.0, 2.0, seed=32))
+    m, s_, t = (A.DeviceBuffer(rows * n * 4) for _ in range(3))
+    shape = A.ints([rows, n])
+    dense, row_b = A.sizes([n, 1]), A.sizes([0, 1])
+    big = rows * n * 4
+    ops = {
+        "mul_row_broadcast": (lambda st: lib.pt_broadcast(y.ptr, A.FLOAT32, row_b, 0, z.ptr, A.FLOAT32, dense, 0,
+                                                          m.ptr, A.FLOAT32, A.OP["mul"], shape, 2, st),
+                              2 * big + n * 4, "k_binary_f32_rows"),
+        "add": (lambda st: lib.pt_broadcast(x.ptr, A.FLOAT32, dense, 0, m.ptr, A.FLOAT32, dense, 0,
+                                            s_.ptr, A.FLOAT32, A.OP["add"], shape, 2, st),
+                3 * big, "k_binary_f32_contig"),
+        "tanh": (lambda st: lib.pt_unary(s_.ptr, A.FLOAT32, dense, 0, t.ptr, A.OP["tanh"], shape, 2, st),
+                 2 * big, "k_unary_f32_contig"),
+    }
+    results = {}
+    for name, (fn, nbytes, kernel) in ops.items():
+        tm = GraphTimer(lambda stream, r, fn=fn: A.check(fn(stream), name), reps=4)
+        tm.run(max(1, warmup))
+        ms = tm.run(max(1, steps))
+        tm.close()
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        results[name] = {"ms": ms, "bytes": nbytes, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "kernel": kernel}
+        log(f"eager {name}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM")
+    total_ms = sum(r["ms"] for r in results.values())
+    total_b = sum(r["bytes"] for r in results.values())
+    return {"workload": "config3 eager: m = y*z, s = x + m, t = tanh(s); x,z [16384,8192] U(-2,2), y [8192]",
+            "ms_per_step": total_ms, "GB/s": total_b / (total_ms * 1e-3) / 1e9,
+            "frac": total_b / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "ops": results}
+
+
 def fused_cpu_baseline(sample_rows=512):
     """Oracle tanh(x + y*z) (per-op rounding, libm tanhf, 1 thread) on a row sample."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -402,7 +441,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="reduce,fused,gemm,mlp")
+    ap.add_argument("--only", default="reduce,fused,gemm,mlp,eager")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 128 MiB device copy first (reference for PMC byte counters)")
@@ -437,6 +476,8 @@ def main():
     extra = {}
     if "mlp" in only:
         extra["mlp"] = mlp_family(max(1, args.steps // 2), args.warmup)
+    if "eager" in only:
+        extra["eager"] = eager_family(args.steps, args.warmup)
     wall = time.perf_counter() - t_wall
 
     # dominant kernel (largest time in a step) for the roofline object
@@ -496,6 +537,7 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
         "config5_mlp": extra.get("mlp"),
+        "config3_eager": extra.get("eager"),
         "cpu_baseline": cpu,
         "wall_s": round(wall, 2),
     }

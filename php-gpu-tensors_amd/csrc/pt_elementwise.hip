@@ -38,6 +38,40 @@ struct EwShape {
     long long total;
 };
 
+// 32-bit form of an EwShape, used when the element count and every
+// operand's largest offset stay below 2^31: index decoding then costs 32-bit
+// divisions instead of emulated 64-bit ones.
+struct EwShape32 {
+    int ndims;
+    unsigned shape[PT_MAX_DIMS];
+    unsigned sa[PT_MAX_DIMS];
+    unsigned sb[PT_MAX_DIMS];
+    unsigned sc[PT_MAX_DIMS];
+    unsigned total;
+};
+
+static bool to32(const EwShape &s, EwShape32 &o)
+{
+    const long long lim = 0x7fffffffLL;
+    if (s.total > lim) return false;
+    long long ma = 0, mb = 0, mc = 0;
+    for (int d = 0; d < s.ndims; d++) {
+        ma += (s.shape[d] - 1) * s.sa[d];
+        mb += (s.shape[d] - 1) * s.sb[d];
+        mc += (s.shape[d] - 1) * s.sc[d];
+    }
+    if (ma > lim || mb > lim || mc > lim) return false;
+    o.ndims = s.ndims;
+    o.total = (unsigned)s.total;
+    for (int d = 0; d < s.ndims; d++) {
+        o.shape[d] = (unsigned)s.shape[d];
+        o.sa[d] = (unsigned)s.sa[d];
+        o.sb[d] = (unsigned)s.sb[d];
+        o.sc[d] = (unsigned)s.sc[d];
+    }
+    return true;
+}
+
 // Merge dims so that each operand's addressing stays affine; drop extent-1.
 static void collapse(const int *shape, int ndims, const size_t *sa, const size_t *sb,
                      const size_t *sc, EwShape &o)
@@ -192,26 +226,29 @@ __device__ __forceinline__ CT bin_op(int op, CT a, CT b)
 // truncate on store, which equals wrapping arithmetic in the narrow type for
 // + - * (modular), and is exact for comparisons / max / min.
 
-__device__ __forceinline__ long long offset_of(const EwShape &s, const long long *st, long long i)
+template <typename SH, typename IT>
+__device__ __forceinline__ IT offset_of(const SH &s, const IT *st, IT i)
 {
-    long long off = 0;
+    IT off = 0;
     for (int d = s.ndims - 1; d >= 0; d--) {
-        long long e = s.shape[d];
-        long long c = i % e;
-        i /= e;
-        off += c * st[d];
+        IT e = s.shape[d];
+        IT q = i / e;
+        off += (i - q * e) * st[d];
+        i = q;
     }
     return off;
 }
 
-template <typename CT>
+// SH: EwShape (64-bit indices) or EwShape32.
+template <typename CT, typename SH>
 __global__ __launch_bounds__(256) void k_binary(const void *__restrict__ a, int dta,
                                                 const void *__restrict__ b, int dtb,
                                                 void *__restrict__ out, int dto, int op,
-                                                EwShape s, int b_scalar, CT scalar, int reverse)
+                                                SH s, int b_scalar, CT scalar, int reverse)
 {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    using IT = decltype(s.total);
+    IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x;
+    const IT stride = (IT)gridDim.x * blockDim.x;
     for (; i < s.total; i += stride) {
         CT x = ld<CT>(a, dta, offset_of(s, s.sa, i));
         CT y = b_scalar ? scalar : ld<CT>(b, dtb, offset_of(s, s.sb, i));
@@ -250,6 +287,41 @@ __global__ __launch_bounds__(256) void k_binary_f32_contig(const float *__restri
     }
 }
 
+// float32 operands over a 2-D [rows, cols] output (cols a multiple of 4):
+// each operand either walks the row (column stride 1, 16-byte loads) or
+// holds one value per row (column stride 0); its row stride may be 0 (a
+// broadcast row).  Operands read once per output element stream past the
+// caches (nontemporal); broadcast ones use ordinary loads.
+__device__ __forceinline__ f32x4 ld_row4(const float *p, unsigned ro, unsigned c, int inner, bool stream)
+{
+    if (!inner) {
+        const float v = p[ro];
+        return (f32x4){v, v, v, v};
+    }
+    return stream ? ld_stream(p + ro + c) : *(const f32x4 *)(p + ro + c);
+}
+
+__global__ __launch_bounds__(256) void k_binary_f32_rows(const float *__restrict__ a, const float *__restrict__ b,
+                                                         float *__restrict__ out, int op, unsigned rows,
+                                                         unsigned cols4, unsigned ra, int ia, unsigned rb, int ib,
+                                                         int reverse)
+{
+    const unsigned g = blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= rows * cols4) return;
+    const unsigned r = g / cols4, c = (g - r * cols4) * 4;
+    const f32x4 x = ld_row4(a, r * ra, c, ia, ia && ra != 0);
+    const f32x4 y = ld_row4(b, r * rb, c, ib, ib && rb != 0);
+    f32x4 v;
+    if (reverse) {
+        v.x = bin_op<float>(op, y.x, x.x); v.y = bin_op<float>(op, y.y, x.y);
+        v.z = bin_op<float>(op, y.z, x.z); v.w = bin_op<float>(op, y.w, x.w);
+    } else {
+        v.x = bin_op<float>(op, x.x, y.x); v.y = bin_op<float>(op, x.y, y.y);
+        v.z = bin_op<float>(op, x.z, y.z); v.w = bin_op<float>(op, x.w, y.w);
+    }
+    st_stream(out + (size_t)g * 4, v);
+}
+
 // ------------------------------------------------------------------ unary
 template <typename CT>
 __device__ __forceinline__ CT unary_f(int op, CT v)
@@ -282,14 +354,15 @@ __device__ __forceinline__ CT unary_f(int op, CT v)
     }
 }
 
-template <typename CT>
+template <typename CT, typename SH>
 __global__ __launch_bounds__(256) void k_unary(const void *__restrict__ x, int dt,
-                                               void *__restrict__ out, int op, EwShape s)
+                                               void *__restrict__ out, int op, SH s)
 {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    using IT = decltype(s.total);
+    IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x;
+    const IT stride = (IT)gridDim.x * blockDim.x;
     for (; i < s.total; i += stride) {
-        long long off = offset_of(s, s.sa, i);
+        IT off = offset_of(s, s.sa, i);
         if constexpr (sizeof(CT) == 8 && (CT)0.5 == (CT)0) {
             // integers: abs/neg exact, floor/ceil/round identity, the rest
             // through float (cuda_op_functors.cuh:153-449)
@@ -347,25 +420,30 @@ __device__ __forceinline__ void cast_elem(const void *x, int dti, long long oi, 
     st<double>(out, dto, i, ld<double>(x, dti, oi));
 }
 
+template <typename SH>
 __global__ __launch_bounds__(256) void k_cast(const void *__restrict__ x, int dti,
-                                              void *__restrict__ out, int dto, EwShape s)
+                                              void *__restrict__ out, int dto, SH s)
 {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
-    for (; i < s.total; i += stride) cast_elem(x, dti, offset_of(s, s.sa, i), out, dto, i);
+    using IT = decltype(s.total);
+    IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x;
+    const IT stride = (IT)gridDim.x * blockDim.x;
+    for (; i < s.total; i += stride) cast_elem(x, dti, (long long)offset_of(s, s.sa, i), out, dto, (long long)i);
 }
 
+template <typename SH>
 __global__ __launch_bounds__(256) void k_where(const void *__restrict__ c, int dtc,
                                                const void *__restrict__ x, const void *__restrict__ y,
-                                               int esz, void *__restrict__ out, EwShape s)
+                                               int esz, void *__restrict__ out, SH s)
 {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    const long long stride = (long long)gridDim.x * blockDim.x;
+    using IT = decltype(s.total);
+    IT i = (IT)blockIdx.x * blockDim.x + threadIdx.x;
+    const IT stride = (IT)gridDim.x * blockDim.x;
     for (; i < s.total; i += stride) {
-        bool pick = ld<double>(c, dtc, offset_of(s, s.sc, i)) != 0.0;
-        if (dtc == PT_INT64 || dtc == PT_UINT64) pick = ((const uint64_t *)c)[offset_of(s, s.sc, i)] != 0;
+        const IT co = offset_of(s, s.sc, i);
+        bool pick = ld<double>(c, dtc, co) != 0.0;
+        if (dtc == PT_INT64 || dtc == PT_UINT64) pick = ((const uint64_t *)c)[co] != 0;
         const void *src = pick ? x : y;
-        long long o = offset_of(s, pick ? s.sa : s.sb, i);
+        IT o = offset_of(s, pick ? s.sa : s.sb, i);
         switch (esz) {
         case 1: ((uint8_t *)out)[i] = ((const uint8_t *)src)[o]; break;
         case 2: ((uint16_t *)out)[i] = ((const uint16_t *)src)[o]; break;
@@ -441,6 +519,25 @@ static long long scalar_as_i64(const pt_scalar_t *s)
     return s->v.i64;
 }
 
+// The 2-D float32 row kernel applies: 1 or 2 collapsed dims, a column
+// count that is a multiple of 4, each operand's column stride 0 or 1, and
+// 16-byte aligned rows for the operands that walk them.
+static bool rows_f32(const EwShape &s, const void *pa, const void *pb, const void *out)
+{
+    if (s.ndims < 1 || s.ndims > 2 || s.total > 0x7fffffffLL) return false;
+    const long long cols = s.shape[s.ndims - 1];
+    if (cols % 4 || ((uintptr_t)out & 15)) return false;
+    const long long ia = s.sa[s.ndims - 1], ib = s.sb[s.ndims - 1];
+    const long long ra = s.ndims == 2 ? s.sa[0] : 0, rb = s.ndims == 2 ? s.sb[0] : 0;
+    if ((ia != 0 && ia != 1) || (ib != 0 && ib != 1)) return false;
+    if (ia == 1 && (((uintptr_t)pa & 15) || ra % 4)) return false;
+    if (ib == 1 && (((uintptr_t)pb & 15) || rb % 4)) return false;
+    const long long rows = s.ndims == 2 ? s.shape[0] : 1;
+    // largest offsets stay in 32 bits
+    if ((rows - 1) * ra + cols > 0x7fffffffLL || (rows - 1) * rb + cols > 0x7fffffffLL) return false;
+    return true;
+}
+
 static pt_status binary_impl(const void *a, int dta, const size_t *sa, size_t offa,
                              const void *b, int dtb, const size_t *sb, size_t offb,
                              const pt_scalar_t *scalar, int reverse, void *out, int dto, int op,
@@ -471,26 +568,32 @@ static pt_status binary_impl(const void *a, int dta, const size_t *sa, size_t of
         float sv = scalar ? (float)scalar_as_double(scalar) : 0.0f;
         k_binary_f32_contig<<<grid_for(s.total, 4), 256, 0, st_>>>(
             (const float *)pa, (const float *)pb, (float *)out, op, s.total, scalar != nullptr, sv, reverse);
+    } else if (!scalar && dta == PT_FLOAT32 && dtb == PT_FLOAT32 && dto == PT_FLOAT32 &&
+               rows_f32(s, pa, pb, out)) {
+        // 2-D row/column broadcasts of float32 (bias adds, row scalings)
+        const unsigned rows = s.ndims == 2 ? (unsigned)s.shape[0] : 1u;
+        const unsigned cols = (unsigned)s.shape[s.ndims - 1];
+        const long long ra = s.ndims == 2 ? s.sa[0] : 0, rb = s.ndims == 2 ? s.sb[0] : 0;
+        const unsigned n4 = rows * (cols / 4);
+        k_binary_f32_rows<<<(n4 + 255) / 256, 256, 0, st_>>>((const float *)pa, (const float *)pb, (float *)out,
+                                                              op, rows, cols / 4, (unsigned)ra,
+                                                              (int)s.sa[s.ndims - 1], (unsigned)rb,
+                                                              (int)s.sb[s.ndims - 1], reverse);
     } else {
+        EwShape32 s32;
+        const bool i32 = to32(s, s32);
+#define PT_BIN(CT, SV)                                                                                          \
+    (i32 ? (k_binary<CT, EwShape32><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto, op, s32, \
+                                                                          scalar != nullptr, SV, reverse), 0) \
+         : (k_binary<CT, EwShape><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto, op, s,     \
+                                                                        scalar != nullptr, SV, reverse), 0))
         switch (compute_class(dto)) {
-        case CT_F32:
-            k_binary<float><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto, op, s,
-                scalar != nullptr, scalar ? (float)scalar_as_double(scalar) : 0.0f, reverse);
-            break;
-        case CT_F64:
-            k_binary<double><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto, op, s,
-                scalar != nullptr, scalar ? scalar_as_double(scalar) : 0.0, reverse);
-            break;
-        case CT_I64:
-            k_binary<long long><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto, op, s,
-                scalar != nullptr, scalar ? scalar_as_i64(scalar) : 0LL, reverse);
-            break;
-        default:
-            k_binary<unsigned long long><<<grid_for(s.total), 256, 0, st_>>>(pa, dta, pb, dtb, out, dto,
-                op, s, scalar != nullptr,
-                scalar ? (unsigned long long)scalar_as_i64(scalar) : 0ULL, reverse);
-            break;
+        case CT_F32: PT_BIN(float, scalar ? (float)scalar_as_double(scalar) : 0.0f); break;
+        case CT_F64: PT_BIN(double, scalar ? scalar_as_double(scalar) : 0.0); break;
+        case CT_I64: PT_BIN(long long, scalar ? scalar_as_i64(scalar) : 0LL); break;
+        default: PT_BIN(unsigned long long, scalar ? (unsigned long long)scalar_as_i64(scalar) : 0ULL); break;
         }
+#undef PT_BIN
     }
     PT_LAUNCH_CHECK("elementwise binary");
     counters().elementwise_calls++;
@@ -539,12 +642,18 @@ pt_status pt_unary(const void *input, int dtype, const size_t *strides, size_t o
     if (contig && dtype == PT_FLOAT32 && ((uintptr_t)px & 15) == 0 && ((uintptr_t)out & 15) == 0) {
         k_unary_f32_contig<<<grid_for(s.total, 4), 256, 0, st_>>>((const float *)px, (float *)out, op, s.total);
     } else {
+        EwShape32 s32;
+        const bool i32 = to32(s, s32);
+#define PT_UN(CT)                                                                                     \
+    (i32 ? (k_unary<CT, EwShape32><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s32), 0) \
+         : (k_unary<CT, EwShape><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s), 0))
         switch (compute_class(dtype)) {
-        case CT_F32: k_unary<float><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s); break;
-        case CT_F64: k_unary<double><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s); break;
-        case CT_I64: k_unary<long long><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s); break;
-        default: k_unary<unsigned long long><<<grid_for(s.total), 256, 0, st_>>>(px, dtype, out, op, s); break;
+        case CT_F32: PT_UN(float); break;
+        case CT_F64: PT_UN(double); break;
+        case CT_I64: PT_UN(long long); break;
+        default: PT_UN(unsigned long long); break;
         }
+#undef PT_UN
     }
     PT_LAUNCH_CHECK("unary");
     counters().elementwise_calls++;
@@ -570,7 +679,9 @@ pt_status pt_cast(const void *input, int dtype_in, const size_t *strides, size_t
                                         hipMemcpyDeviceToDevice, st_), "cast copy"));
         return PT_OK;
     }
-    k_cast<<<grid_for(s.total), 256, 0, st_>>>(px, dtype_in, out, dtype_out, s);
+    EwShape32 s32;
+    if (to32(s, s32)) k_cast<EwShape32><<<grid_for(s.total), 256, 0, st_>>>(px, dtype_in, out, dtype_out, s32);
+    else k_cast<EwShape><<<grid_for(s.total), 256, 0, st_>>>(px, dtype_in, out, dtype_out, s);
     PT_LAUNCH_CHECK("cast");
     counters().elementwise_calls++;
     return PT_OK;
@@ -588,7 +699,12 @@ pt_status pt_where(const void *cond, int dtype_cond, const size_t *strides_cond,
     collapse(shape, ndims, strides_x, strides_y, strides_cond, s);
     if (s.total == 0) return PT_OK;
     hipStream_t st_ = stream_of(stream);
-    k_where<<<grid_for(s.total), 256, 0, st_>>>(cond, dtype_cond, x, y, (int)dtype_size(dtype_xy), out, s);
+    EwShape32 s32;
+    if (to32(s, s32))
+        k_where<EwShape32><<<grid_for(s.total), 256, 0, st_>>>(cond, dtype_cond, x, y, (int)dtype_size(dtype_xy), out,
+                                                               s32);
+    else
+        k_where<EwShape><<<grid_for(s.total), 256, 0, st_>>>(cond, dtype_cond, x, y, (int)dtype_size(dtype_xy), out, s);
     PT_LAUNCH_CHECK("where");
     counters().elementwise_calls++;
     return PT_OK;

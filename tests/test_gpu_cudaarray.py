@@ -75,7 +75,11 @@ def test_full_and_zeros():
 # ----------------------------------------------------------------- binary
 @pytest.mark.parametrize("op", ["ADD", "SUB", "MUL", "DIV"])
 @pytest.mark.parametrize("sa,sb", [((64, 33), (64, 33)), ((64, 33), (33,)), ((5, 1, 7), (1, 6, 7)),
-                                   ((1,), (19, 3)), ((4096,), (4096,))])
+                                   ((1,), (19, 3)), ((4096,), (4096,)),
+                                   # 2-D float32 row kernel: row, column and scalar broadcasts
+                                   ((64, 32), (32,)), ((64, 32), (64, 1)), ((32,), (64, 32)),
+                                   ((3, 5, 8), (5, 8)), ((7, 12), (1, 12)), ((9, 1), (9, 16)),
+                                   ((12,), (1,)), ((300, 1024), (1, 1024))])
 def test_binary_f32_exact(op, sa, sb):
     r = rng(zlib.crc32(repr((op, sa, sb)).encode()))
     a = r.standard_normal(sa).astype(np.float32)
@@ -109,6 +113,22 @@ def test_compare_and_extrema(op):
     ref = ref_fn(a, b).astype(np.float32)
     assert got.getDtype() == "float32"
     np.testing.assert_array_equal(got.toNumpy(), ref)
+
+
+@pytest.mark.parametrize("shape", [(6, 8), (1000, 37), (3, 4, 5, 6)], ids=str)
+def test_strided_views_through_generic_kernels(shape):
+    """Transposed views run the generic index-decoding kernels (32-bit
+    indices at these sizes) for binary, unary, cast and where."""
+    r = rng(11)
+    a = r.standard_normal(shape).astype(np.float32)
+    b = r.standard_normal(shape[::-1]).astype(np.float32)
+    ta, tb = CudaArray.fromNumpy(a), CudaArray.fromNumpy(b).transpose()
+    bt = np.ascontiguousarray(b.transpose())
+    np.testing.assert_array_equal((ta + tb).toNumpy(), O.binary(a, F32, bt, F32, "ADD", F32))
+    np.testing.assert_array_equal(tb.abs().toNumpy(), np.abs(bt))
+    np.testing.assert_array_equal(tb.astype("float64").toNumpy(), bt.astype(np.float64))
+    w = CudaArray.where(tb.gt(0), ta, tb).toNumpy()
+    np.testing.assert_array_equal(w, np.where(bt > 0, a, bt))
 
 
 def test_division_promotes_integers_to_float():
