@@ -231,3 +231,76 @@ def test_graph_replays_all_match_eager_after_eager_work():
     for i in range(5):
         _ = (x + float(i)).sum()      # eager work between replays
         assert bits(graph.run(x, y)).tobytes() == ref
+
+
+# ------------------------------------------------- random plans vs eager
+def _random_program(seed):
+    """A random straight-line program over float32 tensors of shapes drawn
+    from one broadcast family ([R, C], [1, C], [R, 1], [C]), mixing binary,
+    scalar, unary and where nodes, row/column reductions, a matmul and
+    views, with several of its values returned (so the planner has to cut,
+    group same-shape roots, inline roots of one kernel into another and
+    order kernels around native steps)."""
+    rng = np.random.default_rng(seed)
+    R, C = int(rng.integers(2, 40)), int(rng.integers(2, 40)) * 4
+    shapes = [(R, C), (1, C), (R, 1), (C,)]
+    inputs = [rng.uniform(0.5, 1.5, s).astype(np.float32) for s in shapes]
+    steps = []
+    for i in range(int(rng.integers(12, 36))):
+        kind = rng.choice(["bin", "bin", "scal", "un", "where", "red", "red", "mm", "view"])
+        steps.append((kind, int(rng.integers(0, 1 << 30))))
+    outs = sorted(set(int(v) for v in rng.integers(0, len(steps), 5)))
+
+    def program(*xs):
+        vals = list(xs)
+        for kind, r in steps:
+            pick = lambda k: vals[(r >> (3 * k)) % len(vals)]  # noqa: E731
+            a, b = pick(0), pick(1)
+            try:
+                if kind == "bin":
+                    op = ["__add__", "__sub__", "__mul__", "maximum", "minimum"][r % 5]
+                    v = getattr(a, op)(b)
+                elif kind == "scal":
+                    v = (a * 0.75 + 0.25) if r % 2 else (2.0 - a)
+                elif kind == "un":
+                    v = [lambda t: t.abs(), lambda t: (t * 0.5).tanh(), lambda t: t.exp().log()][r % 3](a)
+                elif kind == "where":
+                    v = CudaArray.where(a.gt(b), a, b * 0.5)
+                elif kind == "red":
+                    if a.getNdims() != 2:
+                        raise ValueError
+                    ax = r % 2
+                    keep = a.getShape()
+                    keep[ax] = 1
+                    v = (a.sum(ax) if r % 4 < 2 else a.max(ax)).reshape(keep)
+                elif kind == "mm":
+                    if a.getNdims() != 2 or a.getShape()[1] != C:
+                        raise ValueError
+                    v = a.matmul(vals[3].reshape([C, 1]).broadcastTo([C, 4]).copy()) if r % 2 else \
+                        a.matmul(a.transpose())
+                else:
+                    if a.getNdims() != 2:
+                        raise ValueError
+                    v = a.transpose().transpose() if r % 2 else a.reshape([-1]).reshape(a.getShape())
+            except (ValueError, InvalidArgumentException):
+                v = a + 1.0
+            vals.append(v)
+        n = len(xs)
+        return [vals[n + i] for i in outs]
+
+    return inputs, program
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_plans_match_eager_bitwise(seed):
+    inputs, program = _random_program(seed)
+    tins = [CudaArray.fromNumpy(v) for v in inputs]
+    eager = program(*tins)
+    graph = Fusion.compile(program, tins, cudaGraph=True)
+    for rep in range(3):
+        got = graph.run(*tins)
+        got = got if isinstance(got, (list, tuple)) else [got]
+        assert len(got) == len(eager)
+        for g, e in zip(got, eager):
+            assert g.getShape() == e.getShape()
+            np.testing.assert_array_equal(g.toBits(), e.toBits(), err_msg=f"seed {seed} replay {rep}")
