@@ -304,3 +304,48 @@ def test_random_plans_match_eager_bitwise(seed):
         for g, e in zip(got, eager):
             assert g.getShape() == e.getShape()
             np.testing.assert_array_equal(g.toBits(), e.toBits(), err_msg=f"seed {seed} replay {rep}")
+
+
+def test_native_that_allocates_falls_back_to_eager_replays():
+    """layerNorm over a leading axis permutes its operand into a temporary,
+    which cannot be allocated inside a graph capture: the capture is
+    dropped, the plan keeps to eager execution, and every run still equals
+    the eager result."""
+    r = np.random.default_rng(5)
+    x = CudaArray.fromNumpy(r.standard_normal((24, 16)).astype(np.float32))
+    w = CudaArray.fromNumpy(r.standard_normal((16, 8)).astype(np.float32))
+
+    def body(a, b):
+        h = a.matmul(b).layerNorm([0]) * 2.0
+        return [h, h.sum(1)]
+
+    eager = body(x, w)
+    graph = Fusion.compile(body, [x, w], cudaGraph=True)
+    for _ in range(3):
+        got = graph.run(x, w)
+        for g, e in zip(got, eager):
+            np.testing.assert_array_equal(g.toBits(), e.toBits())
+    st = graph.getStats()
+    assert st["executions"] == 3
+    assert st["cudaGraphCompatible"] == 0 and st["graphLaunches"] == 0
+
+
+def test_native_plan_with_workspace_replays_from_graph():
+    """Split-K GEMM and split column reductions inside a captured plan take
+    their scratch from the plan's workspace; replays match eager."""
+    r = np.random.default_rng(6)
+    a = CudaArray.fromNumpy(r.standard_normal((4096, 64)).astype(np.float32))
+    b = CudaArray.fromNumpy(r.standard_normal((4096, 10)).astype(np.float32))
+
+    def body(p, q):
+        g = p.transpose().matmul(q)          # [64,10], K = 4096: split-K
+        return [g * 0.5, q.sum(0), (p * 2.0).sum(0)]   # column reductions over 4096 rows
+
+    eager = body(a, b)
+    graph = Fusion.compile(body, [a, b], cudaGraph=True)
+    for _ in range(4):
+        got = graph.run(a, b)
+        for g, e in zip(got, eager):
+            np.testing.assert_array_equal(g.toBits(), e.toBits())
+    st = graph.getStats()
+    assert st["cudaGraphCompatible"] == 1 and st["graphLaunches"] == 3
