@@ -124,6 +124,7 @@ struct LeafMap {
 
 struct Kernel {
     std::string name;
+    bool dependent = false;       // a root evaluates another root of this kernel inline
     std::vector<int> roots;
     std::vector<int> leaves;      // items read through pointers
     int shape[kMaxDims] = {0};
@@ -803,7 +804,9 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
     // per element; the general kernel's node functions recompute, so inline
     // chains are at most kMaxInline deep).  Each level runs its natives in
     // item order, then one kernel per shape (at most kMaxRoots roots each).
-    constexpr size_t kMaxRoots = 8;
+    // at most 4 outputs per fused step: the reference's region output
+    // budget (fusion_plan.c:352, 381)
+    constexpr size_t kMaxRoots = 4;
     constexpr int kMaxInline = 2;
     const int nitems = (int)p->items.size();
     std::vector<int> level(nitems, -1), depth(nitems, 0);
@@ -836,6 +839,9 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         depth[id] = dp;
         max_level = std::max(max_level, L);
     }
+    std::vector<std::vector<int>> users(nitems);
+    for (int id = 0; id < nitems; id++)
+        for (int a : p->items[id].args) users[a].push_back(id);
     for (int L = 0; L <= max_level; L++) {
         for (int id = 0; id < nitems; id++)
             if (level[id] == L && p->items[id].kind == IT_NATIVE) {
@@ -844,23 +850,67 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
                 st.item = id;
                 p->steps.push_back(st);
             }
-        std::vector<Kernel> ks;
+        // roots of this level by shape, in item order
+        std::vector<std::vector<int>> groups;
         for (int id = 0; id < nitems; id++) {
             if (level[id] != L || p->items[id].kind != IT_ELEM) continue;
-            const Tensor &t = *p->items[id].t;
-            Kernel *k = nullptr;
-            for (Kernel &c : ks)
-                if (c.ndims == t.ndims && std::equal(t.shape, t.shape + t.ndims, c.shape) &&
-                    c.roots.size() < kMaxRoots)
-                    k = &c;
-            if (!k) {
-                ks.emplace_back();
-                k = &ks.back();
-                k->ndims = t.ndims;
-                for (int d = 0; d < t.ndims; d++) k->shape[d] = t.shape[d];
-                k->total = t.numel();
+            std::vector<int> *g = nullptr;
+            for (auto &c : groups)
+                if (same_shape(c[0], id)) g = &c;
+            if (!g) {
+                groups.emplace_back();
+                g = &groups.back();
             }
-            k->roots.push_back(id);
+            g->push_back(id);
+        }
+        std::vector<Kernel> ks;
+        for (auto &g : groups) {
+            // A root cut only for expression cost whose every use lies in
+            // this group is evaluated inline by its users instead of being
+            // written out (as the reference's dependent-output regions keep
+            // their members uncut, fusion_plan.c:381-389).
+            std::vector<int> kept;
+            for (int a : g) {
+                Item &it = p->items[a];
+                bool inline_it = !it.output && it.reason && !strcmp(it.reason, "expression-cost");
+                if (inline_it) {
+                    std::vector<int> stack = {a};
+                    std::vector<char> seen(nitems, 0);
+                    while (!stack.empty() && inline_it) {
+                        int x = stack.back();
+                        stack.pop_back();
+                        for (int u : users[x]) {
+                            if (seen[u]) continue;
+                            seen[u] = 1;
+                            const Item &ui = p->items[u];
+                            if (ui.kind != IT_ELEM) inline_it = false;
+                            else if (!ui.cut) stack.push_back(u);
+                            else if (std::find(g.begin(), g.end(), u) == g.end()) inline_it = false;
+                        }
+                    }
+                }
+                if (inline_it) it.cut = false;
+                else kept.push_back(a);
+            }
+            // at most kMaxRoots roots per kernel, in order
+            for (size_t b = 0; b < kept.size(); b += kMaxRoots) {
+                Kernel k;
+                const Tensor &t = *p->items[kept[b]].t;
+                k.ndims = t.ndims;
+                for (int d = 0; d < t.ndims; d++) k.shape[d] = t.shape[d];
+                k.total = t.numel();
+                for (size_t r = b; r < kept.size() && r < b + kMaxRoots; r++) k.roots.push_back(kept[r]);
+                int outs = 0;
+                for (int r : k.roots) outs += p->items[r].output ? 1 : 0;
+                for (int r : k.roots) {
+                    std::vector<int> deps;
+                    direct_deps(*p, r, deps);
+                    for (int d : deps)
+                        if (std::find(k.roots.begin(), k.roots.end(), d) != k.roots.end() && outs >= 2)
+                            k.dependent = true;
+                }
+                ks.push_back(k);
+            }
         }
         for (Kernel &k : ks) {
             k.name = "fk" + std::to_string(p->kernels.size());
@@ -1491,16 +1541,29 @@ const char *phpt_graph_plan(phpt_graph *g)
 {
     Plan &p = *g->plan;
     std::ostringstream os;
+    // one entry per step, as FusionGraph::getPlan (fusion.c:775-795):
+    // step, root, kind (fused / native), reason, inputs, outputs; plus the
+    // generated kernel's name and variant
+    int n = 0;
     for (Step &st : p.steps) {
         if (st.native) {
             static const char *names[] = {"native-matmul", "native-reduction", "native-reduction",
                                           "native-moments", "native-softmax", "native-layernorm"};
-            os << "native:" << names[p.items[st.item].t->node->native.kind] << ";";
+            const Item &it = p.items[st.item];
+            os << "step=" << n << ",root=" << st.item << ",kind=native,reason=" << names[it.t->node->native.kind]
+               << ",inputs=" << it.args.size() << ",outputs=1;";
         } else {
             Kernel &k = p.kernels[st.kernel];
-            os << "kernel:" << k.name << "(roots=" << k.roots.size() << ",leaves=" << k.leaves.size()
-               << (k.affine ? ",vector" : ",scalar") << ");";
+            const Item &r0 = p.items[k.roots[0]];
+            const char *reason = k.dependent ? "dependent-outputs"
+                                 : r0.output  ? "output"
+                                 : r0.reason  ? r0.reason
+                                              : "dependency";
+            os << "step=" << n << ",root=" << k.roots[0] << ",kind=fused,reason=" << reason
+               << ",inputs=" << k.leaves.size() << ",outputs=" << k.roots.size() << ",name=" << k.name
+               << ",variant=" << (k.affine ? "vector" : "scalar") << ";";
         }
+        n++;
     }
     t_text = os.str();
     return t_text.c_str();

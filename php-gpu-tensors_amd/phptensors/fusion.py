@@ -137,11 +137,18 @@ class FusionGraph:
         return _host.load().phpt_graph_source(self._g).decode()
 
     def getPlan(self):
+        """One dict per step (fusion.c:775-795): step, root, kind ('fused' or
+        'native'), reason, inputs, outputs; fused steps also name their
+        kernel and its variant (vector / scalar)."""
         steps = []
         for part in _host.load().phpt_graph_plan(self._g).decode().split(";"):
-            if part:
-                kind, _, detail = part.partition(":")
-                steps.append({"kind": kind, "detail": detail})
+            if not part:
+                continue
+            entry = {}
+            for kv in part.split(","):
+                k, _, v = kv.partition("=")
+                entry[k] = int(v) if k in ("step", "root", "inputs", "outputs") else v
+            steps.append(entry)
         return steps
 
     def setProfiling(self, enabled):

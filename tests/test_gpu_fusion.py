@@ -114,7 +114,7 @@ def test_tanh_x_plus_y_z_matches_eager_bitwise(dtype):
     assert fused.getDtype() == dtype
     assert bits(fused).tobytes() == bits(eager).tobytes()
     assert graph.getStats()["fusedKernels"] == 1
-    assert [s["kind"] for s in graph.getPlan()] == ["kernel"]
+    assert [s["kind"] for s in graph.getPlan()] == ["fused"]
 
 
 def test_tanh_x_plus_y_z_vs_oracle():
@@ -169,7 +169,7 @@ def test_native_boundaries_inside_plan():
     for f, e in zip(outs, eager):
         assert bits(f).tobytes() == bits(e).tobytes()
     kinds = [s["kind"] for s in graph.getPlan()]
-    assert "native" in kinds and "kernel" in kinds
+    assert "native" in kinds and "fused" in kinds
     assert graph.getStats()["boundaries"] >= 3
 
 
@@ -349,3 +349,82 @@ def test_native_plan_with_workspace_replays_from_graph():
             np.testing.assert_array_equal(g.toBits(), e.toBits())
     st = graph.getStats()
     assert st["cudaGraphCompatible"] == 1 and st["graphLaunches"] == 3
+
+
+# ------------------------------------------- dependent outputs (reference)
+def _check_outputs(actual, expected):
+    for i, (a, e) in enumerate(zip(actual, expected)):
+        assert a.toBuffer() == e.toBuffer(), f"dependent output {i} differs"
+
+
+def test_dependent_outputs_share_one_kernel():
+    """tests/fusion_dependent_outputs.phpt:21-46: three dependent outputs in
+    one fused kernel; rebinding, async runs and retained storage."""
+    x = CudaArray.fromFlatArray([1, 2, 3, 4], [2, 2])
+
+    def body(x):
+        moment = x * 0.9 + 1
+        variance = (x * x + 1).sqrt()
+        return [moment / variance, moment, variance]
+
+    for cuda_graph in (False, True):
+        graph = Fusion.compile(body, [x], cudaGraph=cuda_graph)
+        assert graph.getStats()["fusedKernels"] == 1 and graph.getPlan()[0]["outputs"] == 3
+        assert graph.getPlan()[0]["reason"] == "dependent-outputs"
+        first = graph.run(x)
+        _check_outputs(first, body(x))
+        _check_outputs(graph.run(x * 2), body(x * 2))
+        _check_outputs(first, body(x))
+        _check_outputs(graph.runAsync(x).wait(), body(x))
+    _check_outputs(Fusion.run(lambda: body(x)), body(x))
+
+
+def test_dependent_output_side_exits_and_budget():
+    """tests/fusion_dependent_outputs.phpt:48-97: native side exits,
+    boundary re-entry, mixed dtypes, long chains and six chained outputs;
+    no fused step returns more than four outputs."""
+    x = CudaArray.fromFlatArray([1, 2, 3, 4], [2, 2])
+
+    def six(x):
+        out = []
+        for _ in range(6):
+            x = x + 1
+            out.append(x)
+        return out
+
+    def chain(x):
+        y = x + 1
+        z = y
+        for _ in range(160):
+            z = z + 1
+        return [z, y]
+
+    cases = [
+        lambda x: [((x + 1) * 2) / 3, (x + 1) * 2, (x + 1).sum(0)],
+        lambda x: [(x + 1) * 2, x + 1, (x + 1).sum(0)],
+        lambda x: [(x + 1) + (x + 1).sum(0), x + 1],
+        lambda x: [(x + 1) + (x + 1).transpose(), x + 1],
+        lambda x: [(x + 1).astype("float64") * 2, x + 1],
+        chain,
+        six,
+    ]
+    for body in cases:
+        for cuda_graph in (False, True):
+            graph = Fusion.compile(body, [x], cudaGraph=cuda_graph)
+            first = graph.run(x)
+            _check_outputs(first, body(x))
+            _check_outputs(graph.run(x * 2), body(x * 2))
+            _check_outputs(first, body(x))
+            assert all(step["outputs"] <= 4 for step in graph.getPlan())
+
+
+def test_dependent_outputs_empty_and_non_finite():
+    """tests/fusion_dependent_outputs.phpt:98-120."""
+    empty = CudaArray.zeros([0, 2])
+    body = lambda x: [x + 1 + 1, x + 1]  # noqa: E731
+    _check_outputs(Fusion.compile(body, [empty]).run(empty), body(empty))
+    special = CudaArray.fromFlatArray([float("nan"), float("inf"), float("-inf"), -0.0], [4])
+    body2 = lambda x: [x * 2 + 1, x * 2]  # noqa: E731
+    actual = Fusion.compile(body2, [special]).run(special)
+    for a, e in zip(actual, body2(special)):
+        assert a.toBuffer() == e.toBuffer()

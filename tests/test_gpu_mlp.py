@@ -184,3 +184,19 @@ def test_config5_full_size_step():
     state = opt.initState(params)
     out = mlp.train_batch(xt, yt, params, opt, state, CudaArray.full([1], 1e-3))
     check_step(layers, rows, 5, params, out, x, y)
+
+
+def test_training_plan_groups_adamw_updates_like_the_reference():
+    """tests/classifier_training.phpt:41-49: the training plan of a
+    784-512-256-10 model keeps one fused dependent-output group per
+    parameter (six) and at most 24 fused kernels."""
+    layers = (784, 512, 256, 10)
+    params, xt, yt, x, y = make(128, layers, 3)
+    opt = Optimizer.adamW()
+    inputs = mlp.training_inputs(xt, yt, CudaArray.full([1], 1e-3), params, opt.initState(params))
+    graph = mlp.compile_training_plan(inputs, opt)
+    plan = graph.getPlan()
+    groups = [s for s in plan if s["reason"] == "dependent-outputs"]
+    assert len(groups) == 6
+    assert graph.getStats()["fusedKernels"] <= 24
+    assert all(s["outputs"] <= 4 for s in plan)
