@@ -113,6 +113,7 @@ struct Item {
     int cost = 0;
     bool cut = false;       // materialized
     bool output = false;
+    bool alias = false;     // view handed to a native step as a strided view (no copy)
     const char *reason = nullptr;
 };
 
@@ -166,9 +167,7 @@ struct Plan {
     bool profiling = false;
     size_t profiled = 0;
     uint64_t bind_ns = 0, execute_ns = 0, collect_ns = 0;
-    bool pending = false;
-    pt_event_t done = nullptr;
-    std::vector<TensorP> pending_values;
+    int pending = 0;  // submitted runAsync executions not yet waited for
     // scratch arena of the native steps inside the captured graph, sized by
     // the first (eager, measuring) run
     bool workspace_sized = false;
@@ -222,11 +221,31 @@ static int collect(Plan &p, const TensorP &t, std::map<const Tensor *, int> &ind
     } else if (me.kind == IT_NATIVE) {
         me.cut = true;
         me.reason = "native";
+        // GEMMs and (axis, or contiguous global) reductions read views of
+        // materialized values in place, as the reference's layout aliases do
+        // (fusion_plan.c:462-486); other native steps take a materialized
+        // operand
+        const NativeSpec &ns = t->node->native;
+        const bool aliasing = ns.kind == NAT_MATMUL || ns.kind == NAT_REDUCE || ns.kind == NAT_ARG_REDUCE;
+        const bool global = (ns.kind == NAT_REDUCE || ns.kind == NAT_ARG_REDUCE) && ns.axis == kGlobalAxis;
         for (int a : me.args) {
-            if (p.items[a].kind != IT_ELEM) continue;
+            Item &ai = p.items[a];
+            if (ai.kind != IT_ELEM) continue;
+            bool view = !ai.cut && ai.t->node->kind == N_VIEW;
+            if (view && global) {
+                size_t cs[kMaxDims];
+                contiguous_strides(ai.t->shape, ai.t->ndims, cs);
+                for (int d = 0; d < ai.t->ndims; d++)
+                    if (ai.t->shape[d] != 1 && ai.t->node->view_strides[d] != cs[d]) view = false;
+            }
+            if (!aliasing || !view) {
+                ai.cut = true;
+                if (!ai.reason) ai.reason = "native-input";
+                continue;
+            }
             // a chain of views over a value reaches the native step as a
-            // strided view of that value (no copy): only its base is
-            // materialized
+            // strided view of that value: only its base is materialized
+            ai.alias = true;
             int b = a;
             while (p.items[b].kind == IT_ELEM && !p.items[b].cut && p.items[b].t->node->kind == N_VIEW)
                 b = p.items[b].args[0];
@@ -1184,6 +1203,10 @@ static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<Ten
         for (size_t i = 0; i < vals.size(); i++)
             if (vals[i]) ptrs.push_back(vals[i]->data());
         if (!p.graph || ptrs != p.graph_ptrs) {
+            // a pending execution may still be running the executable graph
+            // that the capture below updates
+            if (p.pending && !check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed"))
+                return false;
             bool captured = false;
             if (!capture_steps(p, vals, native_present, captured)) return false;
             if (captured) {
@@ -1421,10 +1444,6 @@ int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor
 {
     clear_error();
     Plan &p = *g->plan;
-    if (p.pending) {
-        set_runtime("FusionGraph has a pending asynchronous replay; wait() first");
-        return -1;
-    }
     std::vector<TensorP> ins, outs;
     if (!bind(p, inputs, ninputs, ins)) return -1;
     if (!execute(p, ins, outs, true)) return -1;
@@ -1457,49 +1476,73 @@ int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int coun
     return 0;
 }
 
-int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs)
+// FusionExecution (fusion.c:561-692): each submitted run owns its outputs,
+// the inputs it read and an event recorded after its last step; several may
+// be pending at once (they run in submission order on the runtime stream).
+struct phpt_execution {
+    phpt_graph *graph = nullptr;
+    pt_event_t done = nullptr;
+    std::vector<TensorP> values;  // outputs, then the retained inputs
+    int noutputs = 0;
+    bool waited = false;
+};
+
+phpt_execution *phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs)
 {
     clear_error();
     Plan &p = *g->plan;
-    if (p.pending) {
-        set_runtime("FusionGraph already has a pending replay");
-        return -1;
-    }
     std::vector<TensorP> ins, outs;
-    if (!bind(p, inputs, ninputs, ins)) return -1;
-    if (!execute(p, ins, outs, false)) return -1;
-    if (!p.done && !check_status(pt_event_create(&p.done), "event")) return -1;
-    if (!check_status(pt_event_record(p.done, nullptr), "event record")) return -1;
-    p.pending = true;
-    p.pending_values = outs;
-    for (const TensorP &t : ins) p.pending_values.push_back(t);  // inputs retained until wait()
-    return 0;
+    if (!bind(p, inputs, ninputs, ins)) return nullptr;
+    if (!execute(p, ins, outs, false)) return nullptr;
+    auto *e = new phpt_execution();
+    e->graph = g;
+    if (!check_status(pt_event_create(&e->done), "event") ||
+        !check_status(pt_event_record(e->done, nullptr), "event record")) {
+        if (e->done) pt_event_destroy(e->done);
+        delete e;
+        return nullptr;
+    }
+    e->noutputs = (int)outs.size();
+    e->values = outs;
+    for (const TensorP &t : ins) e->values.push_back(t);
+    p.pending++;
+    return e;
 }
 
-int phpt_graph_wait(phpt_graph *g, phpt_tensor **outputs, int noutputs)
+int phpt_execution_wait(phpt_execution *e, phpt_tensor **outputs, int noutputs)
 {
     clear_error();
-    Plan &p = *g->plan;
-    if (!p.pending) {
-        set_runtime("No pending FusionGraph replay");
+    if (!e || e->waited) {
+        set_runtime("FusionExecution has no submitted execution");
         return -1;
     }
-    if (!check_status(pt_event_synchronize(p.done), "Fusion wait failed")) return -1;
+    if (!check_status(pt_event_synchronize(e->done), "Fusion wait failed")) return -1;
+    Plan &p = *e->graph->plan;
     p.synchronizations++;
-    int n = (int)p.outputs.size();
-    for (int i = 0; i < noutputs && i < n; i++) outputs[i] = wrap(p.pending_values[i]);
-    p.pending = false;
-    p.pending_values.clear();
-    return n;
+    p.pending--;
+    e->waited = true;
+    for (int i = 0; i < noutputs && i < e->noutputs; i++) outputs[i] = wrap(e->values[i]);
+    e->values.clear();
+    return e->noutputs;
 }
 
-int phpt_graph_is_finished(phpt_graph *g)
+int phpt_execution_is_finished(phpt_execution *e)
 {
-    Plan &p = *g->plan;
-    if (!p.pending) return 1;
+    if (!e || e->waited) return 1;
     int fin = 0;
-    if (!check_status(pt_event_query(p.done, &fin), "event query")) return -1;
+    if (!check_status(pt_event_query(e->done, &fin), "event query")) return -1;
     return fin;
+}
+
+void phpt_execution_release(phpt_execution *e)
+{
+    if (!e) return;
+    if (!e->waited) {
+        pt_event_synchronize(e->done);
+        e->graph->plan->pending--;
+    }
+    if (e->done) pt_event_destroy(e->done);
+    delete e;
 }
 
 int phpt_graph_num_outputs(phpt_graph *g) { return (int)g->plan->outputs.size(); }
@@ -1509,7 +1552,9 @@ const char *phpt_graph_source(phpt_graph *g) { return g->plan->source.c_str(); }
 const char *phpt_graph_stats(phpt_graph *g)
 {
     Plan &p = *g->plan;
-    size_t boundaries = 0, intermediates = 0;
+    size_t boundaries = 0, intermediates = 0, aliases = 0;
+    for (const Item &it : p.items)
+        if (it.alias && !it.cut) aliases++;
     bool native_present = false;
     for (Step &st : p.steps) {
         if (st.native) {
@@ -1522,15 +1567,15 @@ const char *phpt_graph_stats(phpt_graph *g)
             if (!p.items[r].output) intermediates++;
     std::ostringstream os;
     os << "nodes=" << p.items.size() << ";fusedKernels=" << p.kernels.size() << ";boundaries=" << boundaries
-       << ";executions=" << p.executions << ";executionSteps=" << p.steps.size()
+       << ";viewAliases=" << aliases << ";executions=" << p.executions << ";executionSteps=" << p.steps.size() + aliases
        << ";intermediateBuffers=" << intermediates << ";cacheHit=" << (p.cache_hit ? 1 : 0)
        << ";backend=" << (p.use_graph ? "cuda-graph" : "stream")
        << ";asyncCompatible=1;cudaGraphCompatible=" << (p.graph_compatible ? 1 : 0)
        << ";graphReplay=" << (p.use_graph && !native_present ? 1 : 0)
        << ";graphLaunches=" << p.graph_launches << ";bufferReuses=" << p.buffer_reuses
-       << ";pending=" << (p.pending ? 1 : 0) << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)
+       << ";pending=" << p.pending << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)
        << ";tensorAllocations=" << p.tensor_allocations << ";synchronizations=" << p.synchronizations
-       << ";workspaceBuffers=" << p.cache.size() << ";profiling=" << (p.profiling ? 1 : 0)
+       << ";workspaceBuffers=" << p.cache.size() + (p.workspace ? 1 : 0) << ";profiling=" << (p.profiling ? 1 : 0)
        << ";profiledExecutions=" << p.profiled << ";bindTimeNs=" << p.bind_ns
        << ";executeTimeNs=" << p.execute_ns << ";collectTimeNs=" << p.collect_ns << ";";
     t_text = os.str();
@@ -1545,11 +1590,18 @@ const char *phpt_graph_plan(phpt_graph *g)
     // step, root, kind (fused / native), reason, inputs, outputs; plus the
     // generated kernel's name and variant
     int n = 0;
+    std::vector<char> shown(p.items.size(), 0);
     for (Step &st : p.steps) {
         if (st.native) {
             static const char *names[] = {"native-matmul", "native-reduction", "native-reduction",
                                           "native-moments", "native-softmax", "native-layernorm"};
             const Item &it = p.items[st.item];
+            // layout aliases: views passed to this native step without a copy
+            for (int a : it.args)
+                if (p.items[a].alias && !p.items[a].cut && !shown[a]) {
+                    shown[a] = 1;
+                    os << "step=" << n++ << ",root=" << a << ",kind=view,reason=native-layout-alias,inputs=1,outputs=1;";
+                }
             os << "step=" << n << ",root=" << st.item << ",kind=native,reason=" << names[it.t->node->native.kind]
                << ",inputs=" << it.args.size() << ",outputs=1;";
         } else {
@@ -1569,21 +1621,26 @@ const char *phpt_graph_plan(phpt_graph *g)
     return t_text.c_str();
 }
 
-void phpt_graph_set_profiling(phpt_graph *g, int enabled)
+int phpt_graph_set_profiling(phpt_graph *g, int enabled)
 {
+    clear_error();
     Plan &p = *g->plan;
+    if (p.pending) {
+        set_runtime("Cannot change profiling while FusionGraph executions are pending");
+        return -1;
+    }
     p.profiling = enabled != 0;
     p.profiled = 0;
     p.bind_ns = p.execute_ns = p.collect_ns = 0;
+    return 0;
 }
 
 void phpt_graph_release(phpt_graph *g)
 {
     if (!g) return;
     Plan &p = *g->plan;
-    if (p.pending) pt_event_synchronize(p.done);
+    if (p.pending) pt_stream_synchronize(nullptr);
     if (p.graph) pt_graph_destroy(p.graph);
-    if (p.done) pt_event_destroy(p.done);
     delete g->plan;
     delete g;
 }

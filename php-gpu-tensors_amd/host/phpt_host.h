@@ -88,16 +88,23 @@ int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor
  * reference, whose run() synchronizes per replay (fusion.c:599-641); it
  * exists to time replay throughput. */
 int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count);
-int phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs);
-int phpt_graph_wait(phpt_graph *g, phpt_tensor **outputs, int noutputs);
-int phpt_graph_is_finished(phpt_graph *g);
+/* FusionGraph::runAsync / FusionExecution (fusion.c:561-692): each
+ * submission returns its own execution (NULL on error); several may be
+ * pending for a plan without a captured graph.  wait returns the number of
+ * outputs and fills `outputs`; release waits if needed and frees. */
+typedef struct phpt_execution phpt_execution;
+phpt_execution *phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ninputs);
+int phpt_execution_wait(phpt_execution *e, phpt_tensor **outputs, int noutputs);
+int phpt_execution_is_finished(phpt_execution *e);
+void phpt_execution_release(phpt_execution *e);
 int phpt_graph_num_outputs(phpt_graph *g);
 const char *phpt_graph_source(phpt_graph *g);
 /* Statistics as "key=value;" pairs (FusionGraph::getStats, fusion.c:723-772). */
 const char *phpt_graph_stats(phpt_graph *g);
-/* Steps as "kind:detail;" entries (FusionGraph::getPlan). */
+/* Steps as "key=value,...;" entries (FusionGraph::getPlan, fusion.c:775-795). */
 const char *phpt_graph_plan(phpt_graph *g);
-void phpt_graph_set_profiling(phpt_graph *g, int enabled);
+/* fails (RuntimeException) while executions are pending */
+int phpt_graph_set_profiling(phpt_graph *g, int enabled);
 void phpt_graph_release(phpt_graph *g);
 /* Module cache counters (Fusion::getCacheStats, fusion_cache.c:50-62). */
 const char *phpt_fusion_cache_stats(void);

@@ -56,9 +56,10 @@ SIGNATURES = {
     "phpt_fusion_run_once": (ctypes.c_int, [ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_run": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_replay": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.c_int]),
-    "phpt_graph_run_async": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int]),
-    "phpt_graph_wait": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int]),
-    "phpt_graph_is_finished": (ctypes.c_int, [G]),
+    "phpt_graph_run_async": (ctypes.c_void_p, [G, ctypes.POINTER(T), ctypes.c_int]),
+    "phpt_execution_wait": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(T), ctypes.c_int]),
+    "phpt_execution_is_finished": (ctypes.c_int, [ctypes.c_void_p]),
+    "phpt_execution_release": (None, [ctypes.c_void_p]),
     "phpt_graph_num_outputs": (ctypes.c_int, [G]),
     "phpt_graph_source": (ctypes.c_char_p, [G]),
     "phpt_graph_stats": (ctypes.c_char_p, [G]),

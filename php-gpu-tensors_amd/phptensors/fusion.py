@@ -126,9 +126,10 @@ class FusionGraph:
 
     def runAsync(self, *inputs):
         lib = _host.load()
-        if lib.phpt_graph_run_async(self._g, _handles(inputs), len(inputs)) != 0:
+        e = lib.phpt_graph_run_async(self._g, _handles(inputs), len(inputs))
+        if not e:
             _host.raise_error("FusionGraph::runAsync")
-        return FusionExecution(self)
+        return FusionExecution(self, e)
 
     def getStats(self):
         return _host.parse_kv(_host.load().phpt_graph_stats(self._g))
@@ -152,23 +153,25 @@ class FusionGraph:
         return steps
 
     def setProfiling(self, enabled):
-        _host.load().phpt_graph_set_profiling(self._g, 1 if enabled else 0)
+        if _host.load().phpt_graph_set_profiling(self._g, 1 if enabled else 0) != 0:
+            _host.raise_error("FusionGraph::setProfiling")
 
 
 class FusionExecution:
-    """Pending replay; wait() synchronises and returns the outputs."""
+    """One submitted runAsync; wait() synchronises on it and returns its
+    outputs (fusion.c:561-692).  The graph stays alive while it is held."""
 
-    def __init__(self, graph):
+    def __init__(self, graph, handle):
         self._graph = graph
+        self._e = handle
         self._result = None
 
     def wait(self):
         if self._result is None:
             lib = _host.load()
-            g = self._graph._g
-            n = lib.phpt_graph_num_outputs(g)
+            n = lib.phpt_graph_num_outputs(self._graph._g)
             outs = self._graph._outputs(n)
-            if lib.phpt_graph_wait(g, outs, n) < 0:
+            if lib.phpt_execution_wait(self._e, outs, n) < 0:
                 _host.raise_error("FusionExecution::wait")
             self._result = self._graph._rebuild([CudaArray._wrap(outs[i]) for i in range(n)])
         return self._result
@@ -176,14 +179,15 @@ class FusionExecution:
     def isFinished(self):
         if self._result is not None:
             return True
-        rc = _host.load().phpt_graph_is_finished(self._graph._g)
+        rc = _host.load().phpt_execution_is_finished(self._e)
         if rc < 0:
             _host.raise_error("FusionExecution::isFinished")
         return rc == 1
 
     def __del__(self):
         try:
-            if self._result is None and _host._lib is not None:
-                self.wait()
+            if self._e and _host._lib is not None:
+                _host._lib.phpt_execution_release(self._e)
+                self._e = None
         except Exception:
             pass

@@ -10,6 +10,7 @@ import pytest
 
 import oracle_lib as O
 from phptensors import CudaArray, Fusion, InvalidArgumentException
+from phptensors._abi import RuntimeException
 
 pytestmark = pytest.mark.gpu
 
@@ -376,6 +377,12 @@ def test_dependent_outputs_share_one_kernel():
         _check_outputs(graph.run(x * 2), body(x * 2))
         _check_outputs(first, body(x))
         _check_outputs(graph.runAsync(x).wait(), body(x))
+        if not cuda_graph:
+            one = graph.runAsync(x)
+            two = graph.runAsync(x * 2)
+            _check_outputs(graph.run(x * 3), body(x * 3))
+            _check_outputs(two.wait(), body(x * 2))
+            _check_outputs(one.wait(), body(x))
     _check_outputs(Fusion.run(lambda: body(x)), body(x))
 
 
@@ -428,3 +435,71 @@ def test_dependent_outputs_empty_and_non_finite():
     actual = Fusion.compile(body2, [special]).run(special)
     for a, e in zip(actual, body2(special)):
         assert a.toBuffer() == e.toBuffer()
+
+
+# ------------------------------------------------ layout aliases (reference)
+def test_layout_aliases_and_workspace_expectations():
+    """tests/fusion_workspace.phpt:14-63 restated: views feeding GEMMs and
+    axis reductions are aliased (no copy), a non-contiguous view feeding a
+    global reduction is materialized, batched and integer plans replay."""
+    a = CudaArray([[1, 2], [3, 4]])
+    unused = CudaArray([9])
+    graph = Fusion.compile(lambda x, u: (x + 1).transpose().matmul(x + 1).sum(0) * 2, [a, unused])
+    assert graph.getStats()["viewAliases"] == 1
+    assert "view" in [s["kind"] for s in graph.getPlan()]
+    assert graph.run(a, unused).toArray() == [92.0, 120.0]
+    assert graph.getStats()["workspaceBuffers"] > 0
+    for _ in range(5):
+        assert graph.run(a, unused).toArray() == [92.0, 120.0]
+    with pytest.raises(InvalidArgumentException):
+        graph.run(CudaArray([1]), unused)
+    sliced = CudaArray([[[1, 2], [3, 4]], [[5, 6], [7, 8]]]).select(0, 1)
+    layout = Fusion.compile(lambda x: x.transpose().matmul(x), [sliced])
+    assert layout.getStats()["viewAliases"] == 1
+    assert layout.run(sliced).toArray() == [[74.0, 86.0], [86.0, 100.0]]
+    glob = Fusion.compile(lambda x: x.transpose().sum(), [a])
+    assert glob.getStats()["viewAliases"] == 0
+    assert glob.run(a).toArray() == [10.0]
+    batched = CudaArray.ones([2, 4, 4])
+    batch = Fusion.compile(lambda x: (x + 1).matmul(x) + 1, [batched])
+    for _ in range(20):
+        assert batch.run(batched).toArray()[1][3][3] == 9.0
+    integer = CudaArray([[1, 2], [3, 4]], "int16")
+    mean = Fusion.compile(lambda x: (x + 1).mean(0) * 2, [integer])
+    assert mean.run(integer).getDtype() == "float64"
+    assert mean.run(integer).toArray() == [6.0, 8.0]
+    arg = Fusion.compile(lambda x: (x + 1).argMax(1), [a])
+    assert arg.run(a).toArray() == [1, 1]
+    pend = Fusion.compile(lambda x: x + 1, [a])
+    execution = pend.runAsync(a)
+    with pytest.raises(RuntimeException):
+        pend.setProfiling(True)
+    execution.wait()
+    large = CudaArray.ones([64, 128])
+    twice, thrice = CudaArray.full([64, 128], 2.0), CudaArray.full([64, 128], 3.0)
+    for cuda_graph in (False, True):
+        par = Fusion.compile(lambda x: x.transpose().matmul(x).sum(1) + 1, [large], cudaGraph=cuda_graph)
+        one, two = par.runAsync(large), par.runAsync(twice)
+        assert par.getStats()["pending"] == 2
+        assert par.run(thrice).toArray() == [73729.0] * 128
+        assert large.matmul(large.transpose()).toArray()[0][0] == 128.0
+        assert two.wait().toArray() == [32769.0] * 128
+        assert one.wait().toArray() == [8193.0] * 128
+        assert par.getStats()["pending"] == 0
+
+
+def test_views_inside_plans_reference_values():
+    """tests/fusion_views.phpt:11-23 with its expected values."""
+    base = CudaArray([[10, 20, 30], [40, 50, 60]])
+    sl = base.select(0, 1)
+    assert Fusion.compile(lambda x: x.sum() + 1, [sl]).run(sl).toArray() == [151.0]
+    assert Fusion.run(lambda: sl.sum()).toArray() == [150.0]
+    tr = base.transpose()
+    assert Fusion.compile(lambda x: x.sum(1) * 2, [tr]).run(tr).toArray() == [100.0, 140.0, 180.0]
+    assert Fusion.compile(lambda x: x.neg() + 1, [tr]).run(tr).toArray() == [[-9.0, -39.0], [-19.0, -49.0],
+                                                                              [-29.0, -59.0]]
+    two = CudaArray([2, 3])
+    assert Fusion.compile(lambda x: x.power(x) * 0, [two]).run(two).toArray() == [0.0, 0.0]
+    res = Fusion.run(lambda: (CudaArray([[1, 2], [3, 4]]) + 1).transpose())
+    del base, sl, tr
+    assert (res * 2).toArray() == [[4.0, 8.0], [6.0, 10.0]]
