@@ -654,7 +654,7 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
 {
     std::string params;
     for (size_t l = 0; l < k.leaves.size(); l++) params += "const void* __restrict__ p" + std::to_string(l) + ",";
-    os << "extern \"C\" __global__ void __launch_bounds__(256) " << k.name << "_v(" << params;
+    os << "extern \"C\" __global__ __launch_bounds__(256) void " << k.name << "_v(" << params;
     for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
     const int nd = k.ndims;
     os << "){\nconst unsigned long long n4=" << k.total / 4 << "ULL;\n"
@@ -834,6 +834,25 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         return x.ndims == y.ndims && std::equal(x.shape, x.shape + x.ndims, y.shape);
     };
     int max_level = 0;
+    // outputs already placed, by (level, shape representative): a value cut
+    // for expression cost is evaluated inline only by an output that joins
+    // other outputs of its shape (a dependent-output group, as the
+    // reference's regions); otherwise its consumers read it back, which is
+    // what the cost budget is for
+    std::vector<std::pair<int, int>> placed_outputs;
+    auto outputs_at = [&](int L, int id) {
+        int n = 0;
+        for (auto &po : placed_outputs)
+            if (po.first == L && same_shape(po.second, id)) n++;
+        return n;
+    };
+    auto inlinable = [&](int d, int id) {
+        if (p->items[d].kind != IT_ELEM || !same_shape(d, id)) return false;
+        const Item &di = p->items[d];
+        if (di.reason && !strcmp(di.reason, "expression-cost"))
+            return p->items[id].output && outputs_at(level[d], id) >= 1;
+        return true;
+    };
     for (int id = 0; id < nitems; id++) {
         Item &it = p->items[id];
         if (it.kind != IT_NATIVE && !(it.kind == IT_ELEM && it.cut)) continue;
@@ -842,14 +861,13 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         int L = 0;
         for (int d : deps) {
             bool dn = p->items[d].kind == IT_NATIVE;
-            bool in_line = it.kind == IT_ELEM && !dn && same_shape(d, id);
+            bool in_line = it.kind == IT_ELEM && !dn && inlinable(d, id);
             L = std::max(L, level[d] + (dn || in_line ? 0 : 1));
         }
         int dp = 0;
         if (it.kind == IT_ELEM)
             for (int d : deps)
-                if (p->items[d].kind == IT_ELEM && level[d] == L && same_shape(d, id))
-                    dp = std::max(dp, depth[d] + 1);
+                if (level[d] == L && inlinable(d, id)) dp = std::max(dp, depth[d] + 1);
         if (dp > kMaxInline) {
             L++;
             dp = 0;
@@ -857,6 +875,7 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         level[id] = L;
         depth[id] = dp;
         max_level = std::max(max_level, L);
+        if (it.kind == IT_ELEM && it.output) placed_outputs.push_back({L, id});
     }
     std::vector<std::vector<int>> users(nitems);
     for (int id = 0; id < nitems; id++)
@@ -889,9 +908,12 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
             // written out (as the reference's dependent-output regions keep
             // their members uncut, fusion_plan.c:381-389).
             std::vector<int> kept;
+            int group_outputs = 0;
+            for (int a : g) group_outputs += p->items[a].output ? 1 : 0;
             for (int a : g) {
                 Item &it = p->items[a];
-                bool inline_it = !it.output && it.reason && !strcmp(it.reason, "expression-cost");
+                bool inline_it = group_outputs >= 2 && !it.output && it.reason &&
+                                 !strcmp(it.reason, "expression-cost");
                 if (inline_it) {
                     std::vector<int> stack = {a};
                     std::vector<char> seen(nitems, 0);

@@ -16,19 +16,32 @@ from ._abi import InvalidArgumentException, RuntimeException  # noqa: F401
 
 
 def _flatten(result):
-    """Tensors of a callback result, in order, and a rebuild function."""
+    """Tensors of a callback result, in order, and a rebuild function.  The
+    result is a CudaArray or a (nested) list, tuple or dict of them, as the
+    reference's output arrays may nest (fusion_boundaries.phpt:22-26)."""
     if isinstance(result, CudaArray):
         return [result], lambda ts: ts[0]
-    if isinstance(result, (list, tuple)):
-        kind = type(result)
-        if not all(isinstance(v, CudaArray) for v in result):
-            raise InvalidArgumentException("Fusion outputs must be CudaArray values")
-        return list(result), lambda ts: kind(ts)
-    if isinstance(result, dict):
-        keys = list(result)
-        if not all(isinstance(result[k], CudaArray) for k in keys):
-            raise InvalidArgumentException("Fusion outputs must be CudaArray values")
-        return [result[k] for k in keys], lambda ts: dict(zip(keys, ts))
+    if isinstance(result, (list, tuple, dict)):
+        items = list(result.items()) if isinstance(result, dict) else list(enumerate(result))
+        if not items and not isinstance(result, dict):
+            return [], lambda ts: type(result)()
+        parts = []
+        tensors = []
+        for key, value in items:
+            sub, rebuild = _flatten(value)
+            parts.append((key, len(sub), rebuild))
+            tensors.extend(sub)
+
+        def rebuild_all(ts):
+            pos, out = 0, []
+            for key, count, rb in parts:
+                out.append((key, rb(ts[pos:pos + count])))
+                pos += count
+            if isinstance(result, dict):
+                return dict(out)
+            return type(result)(v for _, v in out)
+
+        return tensors, rebuild_all
     raise InvalidArgumentException("Fusion callbacks must return a CudaArray or an array of CudaArray")
 
 

@@ -503,3 +503,42 @@ def test_views_inside_plans_reference_values():
     res = Fusion.run(lambda: (CudaArray([[1, 2], [3, 4]]) + 1).transpose())
     del base, sl, tr
     assert (res * 2).toArray() == [[4.0, 8.0], [6.0, 10.0]]
+
+
+def test_boundaries_reference_values():
+    """tests/fusion_boundaries.phpt:11-37 with its expected values."""
+    a = CudaArray([[1, 2], [3, 4]])
+    b = CudaArray([[5, 6], [7, 8]])
+    g = Fusion.compile(lambda a, b: (a * 2 + 1).matmul(b) * 3 + 2, [a, b])
+    st = g.getStats()
+    assert (st["fusedKernels"], st["boundaries"], g.getSource().count("__global__ void")) == (2, 1, 2)
+    assert g.run(a, b).toArray() == ((a * 2 + 1).matmul(b) * 3 + 2).toArray()
+    g = Fusion.compile(lambda a: (a * 2 + 1).sum(1) * 3, [a])
+    assert (g.getStats()["fusedKernels"], g.getStats()["boundaries"]) == (2, 1)
+    assert g.run(a).toArray() == [24.0, 48.0]
+    assert Fusion.compile(lambda a: (a + 1).sum() * 2, [a]).run(a).toArray() == [28.0]
+
+    def nested(a):
+        x = a * 2
+        return {"x": x, "y": [x + 1]}
+
+    out = Fusion.compile(nested, [a]).run(a)
+    assert out["y"][0].toArray() == (a * 2 + 1).toArray() and out["x"].toArray() == (a * 2).toArray()
+
+    def seventy(a):
+        for _ in range(70):
+            a = a + 1
+        return a
+
+    g = Fusion.compile(seventy, [a])
+    assert g.getStats()["fusedKernels"] > 1
+    assert g.run(a).toArray() == [[71.0, 72.0], [73.0, 74.0]]
+    g = Fusion.compile(lambda a: (a * 2).sqrt() + 1, [a])
+    assert g.getStats()["boundaries"] == 0
+    assert g.run(a).toArray() == ((a * 2).sqrt().add(1)).toArray()
+    assert Fusion.compile(lambda a: (a + 1).transpose() * 2, [a]).run(a).toArray() == [[4.0, 8.0], [6.0, 10.0]]
+    view = Fusion.run(lambda: (a + 1).transpose())
+    assert view.getShape() == [2, 2] and (view * 2).getShape() == [2, 2]
+    assert Fusion.compile(lambda a: (a * 2).reshape([4]) + 1, [a]).run(a).toArray() == [3.0, 5.0, 7.0, 9.0]
+    g = Fusion.compile(lambda a: a, [a])
+    assert g.getStats()["fusedKernels"] == 0 and g.run(a).toArray() == a.toArray()
