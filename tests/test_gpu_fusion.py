@@ -542,3 +542,63 @@ def test_boundaries_reference_values():
     assert Fusion.compile(lambda a: (a * 2).reshape([4]) + 1, [a]).run(a).toArray() == [3.0, 5.0, 7.0, 9.0]
     g = Fusion.compile(lambda a: a, [a])
     assert g.getStats()["fusedKernels"] == 0 and g.run(a).toArray() == a.toArray()
+
+
+def test_advanced_reference_expectations():
+    """tests/fusion_advanced.phpt:11-56: unaries, clamp, where, layouts and
+    casts fuse into one kernel each and equal the eager results; grouped
+    outputs; dead nodes are not planned."""
+    a = CudaArray([[1, 2, 3], [4, 5, 6]])
+    b = CudaArray([2, 3, 4])
+    for m in ["neg", "abs", "exp", "sqrt", "log", "sin", "cos", "tan", "floor", "ceil", "round"]:
+        g = Fusion.compile(lambda x: getattr(x + 0.25, m)() + 1, [a])
+        assert g.getStats()["fusedKernels"] == 1 and g.getStats()["boundaries"] == 0, m
+        assert g.run(a).toArray() == getattr(a + 0.25, m)().add(1).toArray(), m
+    c = Fusion.compile(lambda x: (x + 0.5).clamp(2, 4), [a])
+    assert c.getStats()["fusedKernels"] == 1 and c.getStats()["boundaries"] == 0
+    assert c.run(a).toArray() == (a + 0.5).clamp(2, 4).toArray()
+    mask = CudaArray([[1], [0]], "bool")
+    g = Fusion.compile(lambda k, x, y: CudaArray.where(k, x + 1, (x * y).neg()), [mask, a, b])
+    assert g.getStats()["fusedKernels"] == 1
+    assert g.run(mask, a, b).toArray() == CudaArray.where(mask, a + 1, (a * b).neg()).toArray()
+    g = Fusion.compile(lambda x: (x * 2).transpose().astype("float64") + 1, [a])
+    assert g.getStats()["fusedKernels"] == 1
+    expected = [[3.0, 9.0], [5.0, 11.0], [7.0, 13.0]]
+    assert g.run(a).toArray() == expected
+    assert Fusion.run(lambda: (a * 2).transpose().astype("float64") + 1).toArray() == expected
+    assert a.transpose().astype("float64").toArray() == [[1.0, 4.0], [2.0, 5.0], [3.0, 6.0]]
+    g = Fusion.compile(lambda x, y: {"a": (x * y) + 1, "b": (x * y) - 1}, [a, b])
+    assert g.getStats()["fusedKernels"] == 1 and g.getPlan()[0]["outputs"] == 2
+    out = g.run(a, b)
+    assert out["a"].toArray() == (a * b + 1).toArray() and out["b"].toArray() == (a * b - 1).toArray()
+
+    def dead(x):
+        (x + 1).exp()
+        return x * 2
+
+    assert Fusion.compile(dead, [a]).getStats()["nodes"] == 2
+    integer = CudaArray([1, 2, 3], "int16")
+    assert Fusion.run(lambda: (integer + 1).astype("float32")).toArray() == [2.0, 3.0, 4.0]
+
+
+@pytest.mark.parametrize("dtype", ["float32", "float64"])
+def test_power_reference_expectations(dtype):
+    """tests/fusion_power.phpt:16-43: tensor, scalar and inverse-scalar
+    powers fuse into one kernel and match the eager bytes."""
+    base = CudaArray.fromFlatArray([2.0, 4.0, 9.0], [3], dtype)
+    exponent = CudaArray.fromFlatArray([3.0, -2.0, 0.5], [3], dtype)
+    g = Fusion.compile(lambda x, y: (x ** y) + x, [base, exponent])
+    st = g.getStats()
+    assert (st["fusedKernels"], st["executionSteps"], st["intermediateBuffers"]) == (1, 1, 0)
+    fused = g.run(base, exponent)
+    assert fused.getDtype() == dtype and fused.toBuffer() == ((base ** exponent) + base).toBuffer()
+    g = Fusion.compile(lambda x: (x ** -2.0) + (x ** 0.5), [base])
+    assert g.getStats()["fusedKernels"] == 1 and g.getStats()["intermediateBuffers"] == 0
+    assert g.run(base).toBuffer() == ((base ** -2.0) + (base ** 0.5)).toBuffer()
+    g = Fusion.compile(lambda x: (2.0 ** x) + x, [base])
+    assert g.run(base).toBuffer() == ((2.0 ** base) + base).toBuffer()
+    ints = CudaArray([2, 3], "int32")
+    assert Fusion.compile(lambda x: x ** 3, [ints]).run(ints).toBuffer() == (ints ** 3).toBuffer()
+    for low in ("float16", "bfloat16"):
+        v = CudaArray.fromFlatArray([1.5, 2.0, 3.0], [3], low)
+        assert Fusion.compile(lambda x: (x ** 2) + x, [v]).run(v).toBuffer() == ((v ** 2) + v).toBuffer()
