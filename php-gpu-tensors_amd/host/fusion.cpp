@@ -853,6 +853,31 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
             return p->items[id].output && outputs_at(level[d], id) >= 1;
         return true;
     };
+    // A root may read a root of another shape placed at its own level: the
+    // level's kernels then run that shape first (as the reference schedules
+    // a region's cut dependencies before it, fusion_plan.c:104-122).  These
+    // orderings are edges between shape groups of one level and must stay
+    // acyclic; a root that would close a cycle moves one level down.
+    struct Order { int level, before, after; };
+    std::vector<Order> orders;
+    auto precedes = [&](int L, int from, int to) {
+        std::vector<int> stack = {from}, seen;
+        while (!stack.empty()) {
+            int x = stack.back();
+            stack.pop_back();
+            if (same_shape(x, to)) return true;
+            bool visited = false;
+            for (int s : seen) visited = visited || same_shape(s, x);
+            if (visited) continue;
+            seen.push_back(x);
+            for (const Order &o : orders)
+                if (o.level == L && same_shape(o.before, x)) stack.push_back(o.after);
+        }
+        return false;
+    };
+    auto cross = [&](int d, int id) {
+        return p->items[id].kind == IT_ELEM && p->items[d].kind == IT_ELEM && !same_shape(d, id);
+    };
     for (int id = 0; id < nitems; id++) {
         Item &it = p->items[id];
         if (it.kind != IT_NATIVE && !(it.kind == IT_ELEM && it.cut)) continue;
@@ -862,8 +887,13 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         for (int d : deps) {
             bool dn = p->items[d].kind == IT_NATIVE;
             bool in_line = it.kind == IT_ELEM && !dn && inlinable(d, id);
-            L = std::max(L, level[d] + (dn || in_line ? 0 : 1));
+            L = std::max(L, level[d] + (dn || in_line || cross(d, id) ? 0 : 1));
         }
+        for (int d : deps)
+            if (cross(d, id) && level[d] == L && precedes(L, id, d)) {
+                L++;
+                break;
+            }
         int dp = 0;
         if (it.kind == IT_ELEM)
             for (int d : deps)
@@ -875,6 +905,8 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         level[id] = L;
         depth[id] = dp;
         max_level = std::max(max_level, L);
+        for (int d : deps)
+            if (cross(d, id) && level[d] == L) orders.push_back({L, d, id});
         if (it.kind == IT_ELEM && it.output) placed_outputs.push_back({L, id});
     }
     std::vector<std::vector<int>> users(nitems);
@@ -901,6 +933,26 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
             }
             g->push_back(id);
         }
+        // shape groups in an order that honours this level's orderings
+        // (stable: first appearance among the groups that are free to run)
+        std::vector<std::vector<int>> ordered;
+        while (!groups.empty()) {
+            size_t pick = 0;
+            for (size_t c = 0; c < groups.size(); c++) {
+                bool ready = true;
+                for (const Order &o : orders)
+                    if (o.level == L && same_shape(o.after, groups[c][0]))
+                        for (size_t e = 0; e < groups.size(); e++)
+                            if (e != c && same_shape(o.before, groups[e][0])) ready = false;
+                if (ready) {
+                    pick = c;
+                    break;
+                }
+            }
+            ordered.push_back(groups[pick]);
+            groups.erase(groups.begin() + (long)pick);
+        }
+        groups.swap(ordered);
         std::vector<Kernel> ks;
         for (auto &g : groups) {
             // A root cut only for expression cost whose every use lies in

@@ -200,3 +200,85 @@ def test_training_plan_groups_adamw_updates_like_the_reference():
     assert len(groups) == 6
     assert graph.getStats()["fusedKernels"] <= 24
     assert all(s["outputs"] <= 4 for s in plan)
+
+
+# ------------------------------------------- AdamW under Fusion (reference)
+def _adamw_inputs(parameters, gradients, state, rate):
+    return [rate, state["beta1Power"], state["beta2Power"], *parameters, *gradients,
+            *state["firstMoment"], *state["secondMoment"]]
+
+
+def _adamw_tensors(result):
+    st = result["state"]
+    return [*result["parameters"], *st["firstMoment"], *st["secondMoment"], st["beta1Power"], st["beta2Power"]]
+
+
+@pytest.mark.parametrize("dtype,tol", [("float32", 1e-6), ("float64", 1e-12)])
+@pytest.mark.parametrize("cuda_graph", [False, True])
+def test_adamw_fusion_outputs_reference(dtype, tol, cuda_graph):
+    """tests/optimizer_fusion_outputs.phpt:33-115 restated: clipped AdamW
+    recorded by Fusion.compile groups each weight with its two moments,
+    matches the eager step over twelve replays (variable and zero rates,
+    signed clipping boundaries, a strided gradient), keeps earlier outputs
+    and inputs intact, replays asynchronously, rejects a changed gradient
+    shape, and propagates NaN / clips infinities as the eager step does."""
+    from phptensors._abi import InvalidArgumentException
+    opt = Optimizer.adamW(0.001, 0.8, 0.95, 1e-6, 0.02)
+    params = [CudaArray.full([4, 8], 0.25, dtype), CudaArray.full([1, 8], -0.5, dtype)]
+    initial_bytes = [p.toBuffer() for p in params]
+    state = opt.initState(params)
+    ref_params, ref_state = params, state
+    values = [-8.0, -5.0, -4.99, -0.0, 1e-7, 4.99, 5.0, 8.0]
+    grads = [CudaArray.fromFlatArray(values * 4, [8, 4], dtype).transpose(),
+             CudaArray.fromFlatArray(values, [1, 8], dtype)]
+    rate = CudaArray.full([1], 0.001, dtype)
+
+    def body(rate, b1p, b2p, *tensors):
+        p, g, m, v = tensors[0:2], list(tensors[2:4]), tensors[4:6], tensors[6:8]
+        for i, gr in enumerate(g):
+            gr = CudaArray.where(gr.gt(5.0), CudaArray.full([1], 5.0, gr.getDtype()), gr)
+            g[i] = CudaArray.where(gr.lt(-5.0), CudaArray.full([1], -5.0, gr.getDtype()), gr)
+        return opt.step(list(p), g, {"firstMoment": list(m), "secondMoment": list(v),
+                                     "beta1Power": b1p, "beta2Power": b2p}, rate, [True, False])
+
+    graph = Fusion.compile(body, _adamw_inputs(params, grads, state, rate), cudaGraph=cuda_graph)
+    grouped = [s for s in graph.getPlan() if s["kind"] == "fused" and s["outputs"] >= 3]
+    assert len(grouped) >= 2 and graph.getStats()["fusedKernels"] <= 12
+
+    def check(actual, expected):
+        for i, (a, e) in enumerate(zip(_adamw_tensors(actual), _adamw_tensors(expected))):
+            d = (a - e).abs().max().item()
+            assert np.isfinite(d) and d <= tol, (i, d)
+
+    saved = saved_bytes = None
+    for step in range(12):
+        rate = CudaArray.full([1], 0.0 if step == 3 else 0.002 / (step + 1), dtype)
+        sign = -1.0 if step % 2 else 1.0
+        signed = [(grads[0].transpose() * sign).transpose(), grads[1] * sign]
+        expected = body(*_adamw_inputs(ref_params, signed, ref_state, rate))
+        actual = graph.run(*_adamw_inputs(params, signed, state, rate))
+        check(actual, expected)
+        if step == 0:
+            saved = actual
+            saved_bytes = [t.toBuffer() for t in _adamw_tensors(actual)]
+        params, state = actual["parameters"], actual["state"]
+        ref_params, ref_state = expected["parameters"], expected["state"]
+    assert [t.toBuffer() for t in _adamw_tensors(saved)] == saved_bytes
+    assert [p.toBuffer() for p in ref_params] != initial_bytes
+    pending = graph.runAsync(*_adamw_inputs(params, grads, state, rate))
+    expected = body(*_adamw_inputs(params, grads, state, rate))
+    check(pending.wait(), expected)
+    with pytest.raises(InvalidArgumentException):
+        graph.run(*_adamw_inputs(params, [CudaArray.zeros([1], dtype), grads[1]], state, rate))
+    check(graph.run(*_adamw_inputs(params, grads, state, rate)), expected)
+    special = [float("nan"), float("inf"), float("-inf"), -5.0, 5.0, 0.0, 1.0, -1.0]
+    nonfinite = [CudaArray.fromFlatArray(special * 4, [8, 4], dtype).transpose(),
+                 CudaArray.fromFlatArray(special, [1, 8], dtype)]
+    expected = body(*_adamw_inputs(params, nonfinite, state, rate))
+    actual = graph.run(*_adamw_inputs(params, nonfinite, state, rate))
+    for a, e in zip(_adamw_tensors(actual), _adamw_tensors(expected)):
+        av, ev = a.toNumpy().ravel(), e.toNumpy().ravel()
+        assert np.array_equal(np.isnan(av), np.isnan(ev))
+        fin = np.isfinite(ev)
+        assert np.array_equal(av[np.isinf(ev)], ev[np.isinf(ev)])
+        assert np.all(np.abs(av[fin] - ev[fin]) <= tol)
