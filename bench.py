@@ -45,8 +45,8 @@ HBM_PEAK_GBS = 8000.0
 PMC_TRAFFIC_BYTES = {
     "reduce:sum": 134_516_736, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
     "reduce:argmax": 134_535_168, "reduce:var": 134_532_096, "reduce:softmax": 268_549_120,
-    "reduce:layernorm": 269_106_176, "fused:tanh_x_plus_y_z": 1_610_682_624,
-    "gemm:bf16": 1_086_528_192, "gemm:fp16": 1_080_006_976, "gemm:fp32": 2_684_859_904,
+    "reduce:layernorm": 269_131_776, "fused:tanh_x_plus_y_z": 1_610_682_368,
+    "gemm:bf16": 1_086_870_400, "gemm:fp16": 1_079_556_928, "gemm:fp32": 2_684_523_392,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 MALL_BYTES = 256 << 20
