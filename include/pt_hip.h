@@ -73,7 +73,8 @@ enum {
     PT_OP_REDUCE_SUM = 35, PT_OP_REDUCE_MEAN = 36, PT_OP_REDUCE_MAX = 37,
     PT_OP_REDUCE_MIN = 38, PT_OP_REDUCE_PROD = 39,
     PT_OP_ARG_MAX = 42, PT_OP_ARG_MIN = 43,
-    PT_OP_MAXIMUM = 54, PT_OP_MINIMUM = 55
+    PT_OP_MAXIMUM = 54, PT_OP_MINIMUM = 55,
+    PT_OP_REDUCE_ALL = 57, PT_OP_REDUCE_ANY = 58
 };
 
 /* A scalar operand (replaces scalar_value_t, src/data_types.h:38-59):
@@ -155,7 +156,9 @@ pt_status pt_host_free_pinned(void *ptr);
 /* ------------------------------------------------------------ reductions --
  * pt_reduce replaces launch_reduction (src/backends/cuda/reduction_ops.h:
  * 15-22) + cuda_reduction_status (:12): sum/mean/max/min/prod along `axis`
- * (axis < 0: all elements, output shape [1]).  Output dtype as
+ * (axis < 0: all elements, output shape [1]); all/any (OP_REDUCE_ALL / ANY,
+ * cuda_array_ce.c:1791-1823) write bool: every / some element unequal to zero.
+ * Output dtype as
  * ca_private.c:318-324: mean -> float32 for f32/f16/bf16 input, float64 for
  * f64/int/bool; f16/bf16 sum/max/min/prod -> float32 (the reference casts
  * them to float32 first, ca_private.c:297-304); other ops keep the input

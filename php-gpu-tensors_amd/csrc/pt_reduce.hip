@@ -24,7 +24,7 @@
 
 namespace pt {
 
-enum RedOp { R_SUM = 0, R_MEAN, R_MAX, R_MIN, R_PROD, R_ARGMAX, R_ARGMIN, R_VAR };
+enum RedOp { R_SUM = 0, R_MEAN, R_MAX, R_MIN, R_PROD, R_ARGMAX, R_ARGMIN, R_VAR, R_ALL, R_ANY };
 
 // ------------------------------------------------------------------ traits
 // Storage type S, compute type C, 16-byte vector width V.
@@ -744,7 +744,7 @@ __device__ __forceinline__ uint64_t load_u64(const void *p, int dt, size_t i)
 
 __device__ void gen_init(GenAcc &a, int op, int dt)
 {
-    a.op = op; a.dt = dt; a.have = 0; a.u = op == R_PROD ? 1 : 0;
+    a.op = op; a.dt = dt; a.have = 0; a.u = (op == R_PROD || op == R_ALL) ? 1 : 0;
     a.d = op == R_PROD ? 1.0 : (op == R_MAX ? -INFINITY : (op == R_MIN ? INFINITY : 0.0));
     a.si = 0; a.ui = 0; a.m = Mom{0, 0, 0};
     a.best = op == R_ARGMAX ? -INFINITY : INFINITY; a.bi = 0;
@@ -812,6 +812,15 @@ __device__ void gen_add(GenAcc &a, const void *p, size_t off, int idx)
         a.m = mom_combine(a.m, s);
         break;
     }
+    case R_ALL:
+    case R_ANY: {
+        // an element is true when it compares unequal to zero (NaN is true,
+        // -0.0 is false), as AllOpT / AnyOpT, cuda_op_functors.cuh:141-151
+        bool nz = is_float_dt(dt) ? load_as_double(p, dt, off) != 0.0
+                : is_signed_int(dt) ? load_i64(p, dt, off) != 0 : load_u64(p, dt, off) != 0;
+        a.u = a.op == R_ALL ? (a.u && nz) : (a.u || nz);
+        break;
+    }
     }
 }
 
@@ -867,6 +876,12 @@ __device__ void gen_merge(GenAcc &a, const GenAcc &b)
     }
     case R_VAR:
         a.m = mom_combine(a.m, b.m);
+        break;
+    case R_ALL:
+        a.u = a.u && b.u;
+        break;
+    case R_ANY:
+        a.u = a.u || b.u;
         break;
     }
 }
@@ -927,6 +942,10 @@ __device__ void gen_finish(const GenAcc &a, const GenParams &p, void *out, size_
         store_out(out, p.out_dt, o, p.take_sqrt ? sqrt(var) : var);
         break;
     }
+    case R_ALL:
+    case R_ANY:
+        ((uint8_t *)out)[o] = a.u != 0;
+        break;
     }
 }
 
@@ -1230,6 +1249,8 @@ static int red_op_of(int op)
     case PT_OP_REDUCE_PROD: return R_PROD;
     case PT_OP_ARG_MAX: return R_ARGMAX;
     case PT_OP_ARG_MIN: return R_ARGMIN;
+    case PT_OP_REDUCE_ALL: return R_ALL;
+    case PT_OP_REDUCE_ANY: return R_ANY;
     default: return -1;
     }
 }
@@ -1333,6 +1354,7 @@ static bool launch_rows(int dt, int rop, const void *x, size_t rows, int n, size
 static int result_dtype(int dtype, int rop)
 {
     if (rop == R_ARGMAX || rop == R_ARGMIN) return PT_INT32;
+    if (rop == R_ALL || rop == R_ANY) return PT_BOOL;
     if (rop == R_VAR) return (dtype == PT_FLOAT32 || dtype == PT_FLOAT16 || dtype == PT_BFLOAT16)
                           ? PT_FLOAT32 : PT_FLOAT64;
     if (rop == R_MEAN) return (dtype == PT_FLOAT32 || dtype == PT_FLOAT16 || dtype == PT_BFLOAT16)
@@ -1435,7 +1457,7 @@ static pt_status reduce_driver(const void *input, void *output, int dtype, int r
             return fail(PT_ERR_INVALID, "Min/max reduction has no identity for an empty axis");
         if (rop == R_ARGMAX || rop == R_ARGMIN)
             return fail(PT_ERR_INVALID, "Arg reduction has no identity for an empty axis");
-        double ident = rop == R_PROD ? 1.0 : (rop == R_MEAN ? NAN : 0.0);
+        double ident = (rop == R_PROD || rop == R_ALL) ? 1.0 : (rop == R_MEAN ? NAN : 0.0);
         k_fill_identity<<<(unsigned)((outputs + 255) / 256), 256, 0, s>>>(output, out_dt, outputs, ident);
         PT_LAUNCH_CHECK("reduction identity fill");
         return PT_OK;

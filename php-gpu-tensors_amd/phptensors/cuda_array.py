@@ -39,7 +39,7 @@ OP = dict(ADD=0, SUB=1, MUL=2, DIV=3, POW=4, EXP=5, EXPM1=6, SQRT=7, LOG=8, LOG1
           EXP2=10, LOG2=11, LOG10=12, ASIN=13, ACOS=14, ATAN=15, SINH=16, COSH=17,
           TANH=18, SIN=19, COS=20, TAN=21, ABS=22, NEG=23, CEIL=26, FLOOR=27, ROUND=28,
           GT=29, LT=30, EQ=31, NE=32, GE=33, LE=34, SUM=35, MEAN=36, MAX=37, MIN=38,
-          PROD=39, ARG_MAX=42, ARG_MIN=43, MAXIMUM=54, MINIMUM=55)
+          PROD=39, ARG_MAX=42, ARG_MIN=43, MAXIMUM=54, MINIMUM=55, ALL=57, ANY=58)
 
 
 def dtype_code(dtype):
@@ -80,6 +80,63 @@ def _scalar_args(value):
 def _ints(seq):
     seq = [int(v) for v in seq]
     return (ctypes.c_int * max(1, len(seq)))(*seq), len(seq)
+
+
+LN2 = 0.69314718055994530942
+LN10 = 2.30258509299404568402
+
+
+def _unary_backward(op, x, out):
+    """Derivative of each unary operation (autograd.c:1306-1480): logarithms
+    route NaN outside their domain (x < 0, or x < -1 for log1p); rounding has
+    a zero gradient."""
+    def outside(ga, bound):
+        return CudaArray.where(x.lt(bound), CudaArray.full([1], float("nan"), ga.getDtype()), ga)
+
+    if op == OP["EXP"]:
+        return lambda g: [g * out]
+    if op == OP["EXPM1"]:
+        return lambda g: [g * x.exp()]
+    if op == OP["EXP2"]:
+        return lambda g: [g * (out * LN2)]
+    if op == OP["LOG"]:
+        return lambda g: [outside(g / x, 0.0)]
+    if op == OP["LOG1P"]:
+        return lambda g: [outside(g / (x + 1.0), -1.0)]
+    if op == OP["LOG2"]:
+        return lambda g: [outside(g / (x * LN2), 0.0)]
+    if op == OP["LOG10"]:
+        return lambda g: [outside(g / (x * LN10), 0.0)]
+    if op == OP["ASIN"]:
+        return lambda g: [g / (1.0 - x * x).sqrt()]
+    if op == OP["ACOS"]:
+        return lambda g: [-(g / (1.0 - x * x).sqrt())]
+    if op == OP["ATAN"]:
+        return lambda g: [g / (x * x + 1.0)]
+    if op == OP["SINH"]:
+        return lambda g: [g * x.cosh()]
+    if op == OP["COSH"]:
+        return lambda g: [g * x.sinh()]
+    if op == OP["TANH"]:
+        return lambda g: [g * (1.0 - out * out)]
+    if op == OP["SQRT"]:
+        return lambda g: [g / (out * 2.0)]
+    if op == OP["SIN"]:
+        return lambda g: [g * x.cos()]
+    if op == OP["COS"]:
+        return lambda g: [g * -x.sin()]
+    if op == OP["TAN"]:
+        return lambda g: [g / (x.cos() * x.cos())]
+    if op == OP["ABS"]:
+        def abs_back(g):
+            zero = g * 0.0
+            return [CudaArray.where(x.gt(0.0), g, CudaArray.where(x.lt(0.0), -g, zero))]
+        return abs_back
+    if op == OP["NEG"]:
+        return lambda g: [-g]
+    if op in (OP["CEIL"], OP["FLOOR"], OP["ROUND"]):
+        return lambda g: [g * 0.0]
+    return None
 
 
 class CudaArray:
@@ -329,19 +386,10 @@ class CudaArray:
     def _unary(self, op):
         out = CudaArray._wrap(_host.load().phpt_unary(self._h, op))
         if AG.active(self):
-            x = self
-            if op == OP["EXP"]:
-                AG.record(out, [x], lambda g: [g * out], "exp")
-            elif op == OP["LOG"]:
-                AG.record(out, [x], lambda g: [g / x], "log")
-            elif op == OP["NEG"]:
-                AG.record(out, [x], lambda g: [-g], "neg")
-            elif op == OP["SQRT"]:
-                AG.record(out, [x], lambda g: [g / (out * 2.0)], "sqrt")
-            elif op == OP["TANH"]:
-                AG.record(out, [x], lambda g: [g * (1.0 - out * out)], "tanh")
-            else:
+            back = _unary_backward(op, self, out)
+            if back is None:
                 raise InvalidArgumentException("Backward is not implemented for this unary operation")
+            AG.record(out, [self], back, "unary")
         return out
 
     def sqrt(self): return self._unary(OP["SQRT"])
@@ -389,6 +437,15 @@ class CudaArray:
     def max(self, axis=None): return self._reduce(axis, OP["MAX"])
     def min(self, axis=None): return self._reduce(axis, OP["MIN"])
     def prod(self, axis=None): return self._reduce(axis, OP["PROD"])
+
+    def all(self, axis=None):
+        """bool: every element along axis is unequal to zero (cuda_array_ce.c:1791-1806);
+        a discrete output, so no gradient is recorded."""
+        return CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), OP["ALL"]))
+
+    def any(self, axis=None):
+        """bool: some element along axis is unequal to zero (cuda_array_ce.c:1808-1823)."""
+        return CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), OP["ANY"]))
 
     def argMax(self, axis=None):
         return CudaArray._wrap(_host.load().phpt_reduce_arg(self._h, self._axis(axis), OP["ARG_MAX"]))
