@@ -78,11 +78,14 @@ def adamw(params, grads, first, second, beta1_power, beta2_power, lr,
         v = second[i] * beta2 + g * g * (1.0 - beta2)
         upd = (m / c1) / (np.sqrt(v / c2) + eps) * lr
         if weight_decay > 0.0 and mask[i]:
-            out_p.append(p * (1.0 - lr * weight_decay) - upd)
+            newp = p * (1.0 - lr * weight_decay) - upd
         else:
-            out_p.append(p - upd)
-        out_m.append(m)
-        out_v.append(v)
+            newp = p - upd
+        # a NaN gradient keeps the old value (optimizer.c:424-469)
+        keep = np.isnan(g)
+        out_p.append(np.where(keep, p, newp))
+        out_m.append(np.where(keep, first[i], m))
+        out_v.append(np.where(keep, second[i], v))
     return out_p, out_m, out_v, b1p, b2p
 
 

@@ -115,6 +115,7 @@ struct Item {
     bool output = false;
     bool alias = false;     // view handed to a native step as a strided view (no copy)
     const char *reason = nullptr;
+    int region = -1;        // dependent-output region (root item id), or -1
 };
 
 struct LeafMap {
@@ -801,6 +802,132 @@ static pt_module_t load_module(const std::string &src, bool &hit)
     return m;
 }
 
+// ------------------------------------------------------ output regions
+// Dependent-output regions (the reference's fusion_output_regions,
+// fusion_plan.c:250-397, restated): starting from the last output, a region
+// takes every same-shape floating elementwise ancestor of the output (the
+// sum of their operation costs within FUSION_OUTPUT_REGION_BUDGET), then
+// every other output connected to those members, as long as at most four
+// values leave the region (its outputs and members read from outside) and
+// nothing outside it both reads a member and feeds one.  A region of two or
+// more outputs is evaluated by one kernel: its members are not materialized,
+// except those that leave it.
+static constexpr int kRegionBudget = 128;
+
+static bool region_member_kind(const Plan &p, int id, int shape_of)
+{
+    const Item &it = p.items[id];
+    if (it.kind != IT_ELEM || it.region >= 0 || it.alias) return false;
+    const FusionNode &n = *it.t->node;
+    if (n.kind != N_BINARY && n.kind != N_SCALAR && n.kind != N_UNARY && n.kind != N_WHERE &&
+        n.kind != N_CAST)
+        return false;
+    const Tensor &t = *it.t, &r = *p.items[shape_of].t;
+    if (t.dtype != PT_FLOAT32 && t.dtype != PT_FLOAT64 && t.dtype != PT_BOOL) return false;
+    return t.ndims == r.ndims && std::equal(t.shape, t.shape + t.ndims, r.shape);
+}
+
+static int region_op_cost(const Item &it)
+{
+    const FusionNode &n = *it.t->node;
+    int c = n.kind == N_UNARY ? 4 : n.kind == N_WHERE ? 3 : n.op == PT_OP_POW ? 7 : 1;
+    return it.t->dtype == PT_FLOAT64 ? 2 * c : c;
+}
+
+// adds `id` and its compatible ancestors; false when the budget is exceeded
+static bool region_collect(const Plan &p, int id, int shape_of, std::vector<char> &members, int &cost)
+{
+    if (members[id]) return true;
+    if (!region_member_kind(p, id, shape_of)) return true;
+    members[id] = 1;
+    cost += region_op_cost(p.items[id]);
+    if (cost > kRegionBudget) return false;
+    for (int a : p.items[id].args)
+        if (!region_collect(p, a, shape_of, members, cost)) return false;
+    return true;
+}
+
+// true when `id` reaches a member through compatible nodes
+static bool region_connected(const Plan &p, int id, int shape_of, const std::vector<char> &members,
+                             std::vector<char> &seen)
+{
+    if (members[id]) return true;
+    if (seen[id] || !region_member_kind(p, id, shape_of)) return false;
+    seen[id] = 1;
+    for (int a : p.items[id].args)
+        if (region_connected(p, a, shape_of, members, seen)) return true;
+    return false;
+}
+
+// true when `id` reaches a member through any nodes
+static bool region_reenters(const Plan &p, int id, const std::vector<char> &members, std::vector<char> &seen)
+{
+    if (members[id]) return true;
+    if (seen[id]) return false;
+    seen[id] = 1;
+    for (int a : p.items[id].args)
+        if (region_reenters(p, a, members, seen)) return true;
+    return false;
+}
+
+static void output_regions(Plan &p)
+{
+    const int n = (int)p.items.size();
+    for (int root = n - 1; root >= 0; root--) {
+        const Item &ri = p.items[root];
+        if (!ri.output || ri.region >= 0 || ri.kind != IT_ELEM ||
+            (ri.t->dtype != PT_FLOAT32 && ri.t->dtype != PT_FLOAT64))
+            continue;
+        std::vector<char> members(n, 0);
+        int cost = 0;
+        if (!region_collect(p, root, root, members, cost) || !members[root]) continue;
+        for (bool grew = true; grew;) {
+            grew = false;
+            for (int i = 0; i < n; i++) {
+                if (!p.items[i].output || members[i]) continue;
+                std::vector<char> seen(n, 0);
+                if (!region_connected(p, i, root, members, seen)) continue;
+                std::vector<char> trial = members;
+                int trial_cost = cost;
+                if (!region_collect(p, i, root, trial, trial_cost)) continue;
+                int returned = 0;
+                for (int j = 0; j < n; j++) returned += trial[j] && p.items[j].output;
+                if (returned > 4) continue;
+                members.swap(trial);
+                cost = trial_cost;
+                grew = true;
+            }
+        }
+        std::vector<char> leaves_region(n, 0), seen(n, 0);
+        int returned = 0;
+        bool compatible = true;
+        for (int i = 0; i < n && compatible; i++) {
+            if (members[i] && p.items[i].output) {
+                leaves_region[i] = 1;
+                returned++;
+            }
+            for (int c : p.items[i].args) {
+                if (!members[i] && members[c]) leaves_region[c] = 1;
+                if (members[i] && !members[c] && region_reenters(p, c, members, seen)) compatible = false;
+            }
+        }
+        int leaving = 0;
+        for (int i = 0; i < n; i++) leaving += leaves_region[i];
+        if (!compatible || returned < 2 || leaving > 4) continue;
+        for (int i = 0; i < n; i++)
+            if (members[i]) {
+                Item &m = p.items[i];
+                m.region = root;
+                if (leaves_region[i]) {
+                    m.cut = true;
+                    if (!m.output) m.reason = "dependent-outputs";
+                } else {
+                    m.cut = false;
+                }
+            }
+    }
+}
+
 // ------------------------------------------------------------ plan build
 static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<TensorP> &inputs)
 {
@@ -814,6 +941,7 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
     }
     for (int id : p->outputs)
         if (p->items[id].kind == IT_ELEM) p->items[id].cut = true;
+    output_regions(*p);
     // Schedule by levels (as soon as possible).  A native step runs one
     // level after the kernels it reads (at the level of natives it reads);
     // a materialized elementwise root runs one level after kernel roots of
@@ -985,22 +1113,58 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
                 if (inline_it) it.cut = false;
                 else kept.push_back(a);
             }
-            // at most kMaxRoots roots per kernel, in order
-            for (size_t b = 0; b < kept.size(); b += kMaxRoots) {
+            // at most kMaxRoots roots per kernel, in order; the roots of one
+            // region stay together
+            std::vector<std::vector<int>> chunks(1);
+            std::vector<char> placed(kept.size(), 0);
+            for (size_t a = 0; a < kept.size(); a++) {
+                if (placed[a]) continue;
+                std::vector<int> unit;
+                const int reg = p->items[kept[a]].region;
+                for (size_t b2 = a; b2 < kept.size(); b2++)
+                    if (!placed[b2] && (b2 == a || (reg >= 0 && p->items[kept[b2]].region == reg))) {
+                        unit.push_back(kept[b2]);
+                        placed[b2] = 1;
+                    }
+                if (chunks.back().size() + unit.size() > kMaxRoots && !chunks.back().empty())
+                    chunks.emplace_back();
+                chunks.back().insert(chunks.back().end(), unit.begin(), unit.end());
+            }
+            for (const std::vector<int> &chunk : chunks) {
+                if (chunk.empty()) continue;
                 Kernel k;
-                const Tensor &t = *p->items[kept[b]].t;
+                const Tensor &t = *p->items[chunk[0]].t;
                 k.ndims = t.ndims;
                 for (int d = 0; d < t.ndims; d++) k.shape[d] = t.shape[d];
                 k.total = t.numel();
-                for (size_t r = b; r < kept.size() && r < b + kMaxRoots; r++) k.roots.push_back(kept[r]);
+                k.roots = chunk;
                 int outs = 0;
                 for (int r : k.roots) outs += p->items[r].output ? 1 : 0;
-                for (int r : k.roots) {
-                    std::vector<int> deps;
-                    direct_deps(*p, r, deps);
-                    for (int d : deps)
-                        if (std::find(k.roots.begin(), k.roots.end(), d) != k.roots.end() && outs >= 2)
+                // A kernel of two or more outputs is a dependent-output group
+                // when a root reads another root, or two roots evaluate a
+                // common same-shape node inline (the reference's regions join
+                // outputs connected through shared members,
+                // fusion_plan.c:288-301, 337-358).
+                std::vector<int> owner(nitems, -1);
+                for (size_t ri = 0; ri < k.roots.size() && outs >= 2 && !k.dependent; ri++) {
+                    const int r = k.roots[ri];
+                    std::vector<int> stack(p->items[r].args.begin(), p->items[r].args.end());
+                    std::vector<char> seen(nitems, 0);
+                    while (!stack.empty() && !k.dependent) {
+                        int x = stack.back();
+                        stack.pop_back();
+                        if (seen[x]) continue;
+                        seen[x] = 1;
+                        if (std::find(k.roots.begin(), k.roots.end(), x) != k.roots.end()) {
                             k.dependent = true;
+                            break;
+                        }
+                        const Item &xi = p->items[x];
+                        if (xi.kind != IT_ELEM || xi.cut || !same_shape(x, r)) continue;
+                        if (owner[x] >= 0 && owner[x] != (int)ri) k.dependent = true;
+                        owner[x] = (int)ri;
+                        for (int a : xi.args) stack.push_back(a);
+                    }
                 }
                 ks.push_back(k);
             }

@@ -11,6 +11,7 @@ the callback's result structure.
 import ctypes
 
 from . import _host
+from . import autograd as AG
 from .cuda_array import CudaArray
 from ._abi import InvalidArgumentException, RuntimeException  # noqa: F401
 
@@ -85,17 +86,29 @@ class Fusion:
                 raise InvalidArgumentException("Fusion::compile inputs must be CudaArray values")
         if lib.phpt_fusion_begin(1) != 0:
             _host.raise_error("Fusion::compile")
+        tracked = [bool(t._rg) for t in inputs]
         try:
             placeholders = [CudaArray._wrap(lib.phpt_fusion_input(t._h, i)) for i, t in enumerate(inputs)]
+            # placeholders keep the examples' requiresGrad (fusion.c:357)
+            for ph, rg in zip(placeholders, tracked):
+                ph._rg = rg
             result = callback(*placeholders)
             outs, rebuild = _flatten(result)
+            # a tracked output must have run backward() inside the callback
+            # (fusion.c:376-387)
+            if any(AG.needs_grad(t) for t in outs):
+                raise InvalidArgumentException(
+                    "Fusion::compile() cannot detach tracked outputs implicitly; call backward() inside "
+                    "the callback or detach() the output explicitly")
         except BaseException:
             lib.phpt_fusion_abort()
             raise
         g = lib.phpt_fusion_end(_handles(outs), len(outs), 1 if cudaGraph else 0)
         if not g:
             _host.raise_error("Fusion::compile")
-        return FusionGraph(g, rebuild, len(inputs))
+        graph = FusionGraph(g, rebuild, len(inputs))
+        graph._tracked = tracked
+        return graph
 
     @staticmethod
     def getCacheStats():
@@ -113,6 +126,16 @@ class FusionGraph:
         self._g = handle
         self._rebuild = rebuild
         self._ninputs = ninputs
+        self._tracked = [False] * ninputs
+
+    def _check_tracking(self, inputs):
+        """An input may not enable gradients its example lacked at capture
+        (fusion.c:479-486)."""
+        for i, (t, rg) in enumerate(zip(inputs, self._tracked)):
+            if isinstance(t, CudaArray) and t._rg and not rg:
+                raise InvalidArgumentException(
+                    f"FusionGraph input {i} enables gradients absent from capture; enable requiresGrad() "
+                    "before compile and capture backward(), or detach() the input")
 
     def __del__(self):
         g = getattr(self, "_g", None)
@@ -124,6 +147,7 @@ class FusionGraph:
         return (ctypes.c_void_p * max(1, count))()
 
     def run(self, *inputs):
+        self._check_tracking(inputs)
         lib = _host.load()
         n = lib.phpt_graph_num_outputs(self._g)
         outs = self._outputs(n)
@@ -138,6 +162,7 @@ class FusionGraph:
             _host.raise_error("FusionGraph::replay")
 
     def runAsync(self, *inputs):
+        self._check_tracking(inputs)
         lib = _host.load()
         e = lib.phpt_graph_run_async(self._g, _handles(inputs), len(inputs))
         if not e:

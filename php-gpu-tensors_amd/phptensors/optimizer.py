@@ -59,20 +59,42 @@ class Optimizer:
             p.zeroGrad()
 
     def step(self, parameters, gradients, state, learningRate=None, weightDecayMask=None):
-        if len(parameters) != len(gradients):
-            raise InvalidArgumentException("One gradient per parameter is required")
+        """Optimizer::step (optimizer.c:730-800): equally long CudaArray lists,
+        each gradient of its parameter's shape and dtype, a boolean decay mask
+        per parameter; the rate is a CudaArray or, when omitted, the
+        optimizer's own."""
+        parameters, gradients = list(parameters), list(gradients)
+        if len(parameters) != len(gradients) or not all(
+                isinstance(t, CudaArray) for t in parameters + gradients):
+            raise InvalidArgumentException("parameters and gradients must be equally sized CudaArray lists")
         for p, g in zip(parameters, gradients):
-            if g is not None and g.getShape() != p.getShape():
-                raise InvalidArgumentException("Gradient shape does not match its parameter")
-        mask = weightDecayMask if weightDecayMask is not None else [True] * len(parameters)
+            if g.getShape() != p.getShape():
+                raise InvalidArgumentException("Each gradient must have the same shape as its parameter")
+            if g.getDtype() != p.getDtype():
+                raise InvalidArgumentException("Each gradient must have the same dtype as its parameter")
+        if weightDecayMask is not None:
+            mask = list(weightDecayMask)
+            if len(mask) != len(parameters):
+                raise InvalidArgumentException("weightDecayMask must match the parameter count")
+            if not all(isinstance(m, bool) for m in mask):
+                raise InvalidArgumentException("weightDecayMask entries must be booleans")
+        else:
+            mask = [True] * len(parameters)
         lr = self.learningRate if learningRate is None else learningRate
         if self.kind == "adamW":
             return self._adamw(parameters, gradients, state, lr, mask)
         return self._sgd(parameters, gradients, state, lr, mask)
 
+    @staticmethod
+    def _selected(g, updated, original, detach):
+        """Where the gradient is NaN the old value is kept (where(g == g, ...),
+        optimizer.c:424-469); updated parameters are detached from the graph."""
+        out = CudaArray.where(g.eq(g), updated, original)
+        return out.detach() if detach else out
+
     def _adamw(self, parameters, gradients, state, lr, mask):
+        """optimizer_adamw_step (optimizer.c:471-607), operation by operation."""
         b1, b2, eps, wd = self.beta1, self.beta2, self.epsilon, self.weightDecay
-        # shared terms (optimizer.c:505-514)
         b1p = state["beta1Power"] * b1
         b2p = state["beta2Power"] * b2
         c1 = (b1p - 1.0) * -1.0
@@ -80,11 +102,6 @@ class Optimizer:
         out_p, out_m, out_v = [], [], []
         for i, (p, g) in enumerate(zip(parameters, gradients)):
             m0, v0 = state["firstMoment"][i], state["secondMoment"][i]
-            if g is None:
-                out_p.append(p)
-                out_m.append(m0)
-                out_v.append(v0)
-                continue
             m = m0 * b1 + g * (1.0 - b1)
             v = v0 * b2 + (g * g) * (1.0 - b2)
             upd = (m / c1) / ((v / c2).sqrt() + eps) * lr
@@ -93,24 +110,22 @@ class Optimizer:
                 newp = p * decay - upd
             else:
                 newp = p - upd
-            out_p.append(newp)
-            out_m.append(m)
-            out_v.append(v)
+            out_p.append(self._selected(g, newp, p, True))
+            out_m.append(self._selected(g, m, m0, False))
+            out_v.append(self._selected(g, v, v0, False))
         return {"parameters": out_p,
                 "state": {"firstMoment": out_m, "secondMoment": out_v, "beta1Power": b1p, "beta2Power": b2p}}
 
     def _sgd(self, parameters, gradients, state, lr, mask):
+        """optimizer_sgd_step (optimizer.c:609-676): the velocity g + v·momentum
+        is the new state; weight decay enters the step only."""
         mom, wd = self.momentum, self.weightDecay
         out_p, out_v = [], []
         for i, (p, g) in enumerate(zip(parameters, gradients)):
-            vel = state["velocity"][i]
-            if g is None:
-                out_p.append(p)
-                out_v.append(vel)
-                continue
-            if wd > 0.0 and mask[i]:
-                g = g + p * wd
-            v = vel * mom + g if mom > 0.0 else g
-            out_p.append(p - v * lr)
-            out_v.append(v)
+            vel0 = state["velocity"][i]
+            vel = g + vel0 * mom
+            direction = vel + p * wd if (wd > 0.0 and mask[i]) else vel
+            newp = p - direction * lr
+            out_p.append(self._selected(g, newp, p, True))
+            out_v.append(self._selected(g, vel, vel0, False))
         return {"parameters": out_p, "state": {"velocity": out_v}}

@@ -8,7 +8,7 @@ import sys
 import numpy as np
 import pytest
 
-from phptensors import CudaArray, Fusion
+from phptensors import CudaArray, Fusion, InvalidArgumentException
 from phptensors import mlp
 from phptensors.optimizer import Optimizer
 
@@ -50,6 +50,64 @@ def test_sgd_closed_form():
     out = sgd.step([p], [p.grad()], st)
     assert abs(out["parameters"][0].item() - 1.6) < 1e-6
     assert out["state"]["velocity"][0].item() == 4.0
+
+
+def test_optimizer_reference_remaining_cases():
+    """optimizer.phpt:32-105: float64 state and update keep float64, a
+    Fusion-compiled SGD step over a tracked parameter (backward inside the
+    callback), a mismatched gradient shape and an invalid beta are refused."""
+    sgd = Optimizer.sgd(0.1, 0.9)
+    dp = CudaArray.fromFlatArray([2.0], [1], "float64").requiresGrad()
+    dstate = sgd.initState([dp])
+    assert dstate["velocity"][0].getDtype() == "float64"
+    sgd.zeroGrad([dp])
+    (dp * dp).sum().backward()
+    dstep = sgd.step([dp], [dp.grad()], dstate)
+    assert dstep["parameters"][0].getDtype() == "float64"
+    fp = CudaArray.fromFlatArray([2.0], [1]).requiresGrad()
+    fstate = sgd.initState([fp])
+    rate = CudaArray.fromFlatArray([0.1], [1])
+
+    def body(parameter, velocity, r):
+        sgd.zeroGrad([parameter])
+        (parameter * parameter).sum().backward()
+        return sgd.step([parameter], [parameter.grad()], {"velocity": [velocity]}, r)
+
+    graph = Fusion.compile(body, [fp, fstate["velocity"][0], rate])
+    fstep = graph.run(fp, fstate["velocity"][0], rate)
+    assert abs(fstep["parameters"][0].item() - 1.6) < 1e-5
+    assert abs(fstep["state"]["velocity"][0].item() - 4.0) < 1e-5
+    p = CudaArray.fromFlatArray([2.0], [1]).requiresGrad()
+    with pytest.raises(InvalidArgumentException):
+        sgd.step([p], [CudaArray.fromFlatArray([1.0, 2.0], [2])], sgd.initState([p]))
+    with pytest.raises(InvalidArgumentException):
+        Optimizer.adamW(0.1, 1.0)
+
+
+@pytest.mark.parametrize("kind", ["adamW", "sgd"])
+def test_nan_gradient_keeps_parameter_and_state(kind):
+    """optimizer.c:424-469: where a gradient is NaN the parameter and its
+    state keep their old values; infinite gradients still update."""
+    opt = Optimizer.adamW(0.1, 0.9, 0.999, 1e-8, 0.1) if kind == "adamW" else Optimizer.sgd(0.1, 0.9, 0.01)
+    p = CudaArray.fromFlatArray([1.0, 2.0, 3.0], [3])
+    state = opt.initState([p])
+    if kind == "adamW":
+        state["firstMoment"] = [CudaArray.fromFlatArray([0.5, 0.5, 0.5], [3])]
+    else:
+        state["velocity"] = [CudaArray.fromFlatArray([0.5, 0.5, 0.5], [3])]
+    g = CudaArray.fromFlatArray([float("nan"), 1.0, float("inf")], [3])
+    out = opt.step([p], [g], state)
+    newp = out["parameters"][0].toArray()
+    assert newp[0] == 1.0 and newp[1] != 2.0
+    if kind == "adamW":
+        m = out["state"]["firstMoment"][0].toArray()
+        assert m[0] == 0.5 and m[1] != 0.5 and m[2] == float("inf")
+        assert out["state"]["secondMoment"][0].toArray()[0] == 0.0
+    else:
+        v = out["state"]["velocity"][0].toArray()
+        assert v[0] == 0.5 and abs(v[1] - 1.45) < 1e-6 and v[2] == float("inf")
+        # weight decay enters the step, not the velocity (optimizer.c:644-660)
+        assert abs(newp[1] - (2.0 - 0.1 * (1.45 + 2.0 * 0.01))) < 1e-6
 
 
 def test_max_gradient_shared_among_ties():
