@@ -765,10 +765,13 @@ struct ModuleCache {
     std::mutex mu;
     std::unordered_map<std::string, pt_module_t> modules;
     std::vector<std::string> order;
-    size_t hits = 0, misses = 0, evictions = 0;
+    size_t hits = 0, misses = 0, evictions = 0, compilations = 0;
+    size_t bytes = 0;  // source text held as keys
 };
 static ModuleCache g_cache;
-static const size_t kCacheEntries = 16;  // fusion_cache.c: 16-entry LRU
+// fusion_cache.c: a 16-entry, 16 MiB LRU (FUSION_CACHE_ENTRIES / _BYTES)
+static const size_t kCacheEntries = 16;
+static const size_t kCacheBytes = 16u << 20;
 
 static pt_module_t load_module(const std::string &src, bool &hit)
 {
@@ -792,9 +795,13 @@ static pt_module_t load_module(const std::string &src, bool &hit)
         return nullptr;
     // modules stay loaded while plans may use them; eviction only drops
     // the cache entry (compiled graphs keep their module handle)
+    g_cache.compilations++;
     g_cache.modules[src] = m;
     g_cache.order.push_back(src);
-    while (g_cache.order.size() > kCacheEntries) {
+    g_cache.bytes += src.size();
+    while (g_cache.order.size() > kCacheEntries ||
+           (g_cache.bytes > kCacheBytes && g_cache.order.size() > 1)) {
+        g_cache.bytes -= g_cache.order.front().size();
         g_cache.modules.erase(g_cache.order.front());
         g_cache.order.erase(g_cache.order.begin());
         g_cache.evictions++;
@@ -1505,6 +1512,10 @@ static bool compile_plan(Plan &p)
 
 bool fusion_materialize(const TensorP &t)
 {
+    if (t->fusion_failed) {
+        set_runtime("Tensor belongs to an aborted Fusion capture");
+        return false;
+    }
     if (!t->lazy()) return true;
     // evaluate the recorded subgraph producing `t` now (Fusion::run reads
     // inside the callback), then keep `t` as a concrete value
@@ -1514,7 +1525,7 @@ bool fusion_materialize(const TensorP &t)
     for (const Item &it : p->items)
         if (it.kind == IT_INPUT) {
             t_scope = saved;
-            set_invalid("Compiled Fusion inputs cannot be read during capture");
+            set_runtime("Fusion::compile cannot read tensor data during capture; use FusionGraph::run");
             return false;
         }
     bool ok = compile_plan(*p);
@@ -1553,7 +1564,7 @@ int phpt_fusion_begin(int compiling)
 {
     clear_error();
     if (t_scope) {
-        set_invalid("Fusion scopes cannot be nested");
+        set_runtime("Fusion scopes cannot be nested");
         return -1;
     }
     t_scope = new Scope();
@@ -1565,6 +1576,11 @@ int phpt_fusion_active(void) { return fusion_active() ? 1 : 0; }
 
 void phpt_fusion_abort(void)
 {
+    // values recorded by the aborted callback can never be computed
+    // (fusion_failed, fusion.c:160-166)
+    if (t_scope)
+        for (const TensorP &t : t_scope->recorded)
+            if (t->lazy()) t->fusion_failed = true;
     delete t_scope;
     t_scope = nullptr;
 }
@@ -1887,17 +1903,24 @@ const char *phpt_fusion_cache_stats(void)
 {
     std::lock_guard<std::mutex> lock(g_cache.mu);
     std::ostringstream os;
-    os << "entries=" << g_cache.modules.size() << ";capacity=" << kCacheEntries << ";hits=" << g_cache.hits
-       << ";misses=" << g_cache.misses << ";evictions=" << g_cache.evictions << ";";
+    // keys of Fusion::getCacheStats (fusion_cache.c:54-61)
+    os << "entries=" << g_cache.modules.size() << ";bytes=" << g_cache.bytes << ";hits=" << g_cache.hits
+       << ";misses=" << g_cache.misses << ";compilations=" << g_cache.compilations
+       << ";evictions=" << g_cache.evictions << ";maxEntries=" << kCacheEntries << ";maxBytes=" << kCacheBytes
+       << ";capacity=" << kCacheEntries << ";";
     t_text = os.str();
     return t_text.c_str();
 }
 
 void phpt_fusion_clear_cache(void)
 {
+    // the cache and its counters start over (fusion_cache_shutdown,
+    // fusion_cache.c:41-48); compiled graphs keep their modules
     std::lock_guard<std::mutex> lock(g_cache.mu);
     g_cache.modules.clear();
     g_cache.order.clear();
+    g_cache.hits = g_cache.misses = g_cache.evictions = g_cache.compilations = 0;
+    g_cache.bytes = 0;
 }
 
 }  // extern "C"

@@ -82,6 +82,7 @@ struct Tensor {
     size_t offset = 0;               // elements
     bool read_only = false;          // broadcast views
     bool is_view = false;            // made by a view operation (shares storage)
+    bool fusion_failed = false;      // recorded in a Fusion scope that was aborted
     std::shared_ptr<FusionNode> node;  // set while recorded in a Fusion scope
     uint64_t id = 0;
 

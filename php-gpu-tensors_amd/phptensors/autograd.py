@@ -91,8 +91,12 @@ def backward(root, gradient=None):
         order.append(t)
 
     visit(root)
+    # fp16 / bf16 roots propagate float32 gradients (autograd.c:1741-1764)
+    low = root.getDtype() in ("float16", "bfloat16")
     if gradient is None:
-        gradient = CudaArray.ones(root.getShape(), root.getDtype())
+        gradient = CudaArray.ones(root.getShape(), "float32" if low else root.getDtype())
+    elif low:
+        gradient = gradient.astype("float32")
     grads = {id(root): gradient}
     _recording[0] = False  # gradients carry no history of their own
     try:
