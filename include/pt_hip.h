@@ -228,19 +228,41 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
                     const int *shape_c, int nd_c, pt_stream_t stream);
 
 /* Precision policy (replaces cuda_blas_set_precision / _precision_name,
- * matmul_kernels.h:31-33).  0 = fp32-strict, 1 = tf32 request (gfx950 has
- * no xf32 MFMA: strict fp32 is used either way and the name reports it). */
+ * matmul_kernels.h:31-33).  0 = fp32-strict (the default); 1 = tf32 is
+ * refused with PT_ERR_UNSUPPORTED, as the reference refuses it on a device
+ * without TF32 (tests/matmul_precision.phpt:51-56): gfx950 has no xf32 MFMA.
+ * Other values: PT_ERR_INVALID.  The mode never changes on an error. */
 pt_status pt_matmul_set_precision(int precision);
 const char *pt_matmul_precision_name(void);
 
 /* Tile override for the MFMA kernels, the tuning knob that replaces
  * cuda_blas_tune_matmul (matmul_kernels.h:34-38): 0 = 256x128, 1 = 128x128,
- * 2 = 64x64, 3 = 256x256 workgroup tiles, 5 = 256x256 with a doubled K
- * step, 8 = 256x256 direct-to-LDS kernel for f16/bf16 (whole tiles, K a
- * multiple of 64, k-contiguous A; other cases run tile 3), 9 = 256x128
- * with 8 waves (the large-problem fp32 choice), -1 = automatic choice
- * (default). */
+ * 2 = 64x64, 3 = 256x256 workgroup tiles, 4 / 5 = 256x128 / 256x256 with a
+ * doubled K step, 6 / 7 = 256x256 with 4 waves (single / doubled K step),
+ * 8 = 256x256 direct-to-LDS kernel for f16/bf16 (whole tiles, K a multiple
+ * of 64, k-contiguous A; other cases run tile 3), 9 = 256x128 with 8 waves
+ * (the large-problem fp32 choice), 10 / 11 = 128x128 with 8 waves (single /
+ * doubled K step), 12 / 13 = 128x64 with 4 waves and two workgroups per CU
+ * (single / doubled K step; the mid-size fp32 choice); 11-13 are fp32 only
+ * and 16-bit requests run 128x128.  -1 = automatic choice (default). */
 pt_status pt_matmul_set_tile(int tile);
+/* Measured tile choice for one problem, the counterpart of
+ * cuda_blas_tune_matmul (matmul_kernels.h:34-38; a cuBLASLt candidate sweep
+ * there, matmul_kernels.cu:336-456).  Every tile configuration built for the
+ * dtype runs once untimed and five times between HIP events on `stream`,
+ * writing `c`; the fastest median is kept for this (dtype, M, N, K, batch,
+ * operand layout) and used by later pt_matmul calls with no tile override
+ * (backend info then reports a "-tuned" matmul).  tiles / median_ms receive
+ * up to max_candidates entries, *count how many were written, *selected the
+ * index of the fastest; `c` ends holding the product.  A problem with
+ * M*N*K below 1e7 is not eligible (PT_ERR_INVALID), as the reference tunes
+ * only its cuBLASLt range. */
+pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
+                         const int *shape_a, const size_t *strides_a, int nd_a,
+                         const int *shape_b, const size_t *strides_b, int nd_b,
+                         const int *shape_c, int nd_c, int *tiles, float *median_ms,
+                         int max_candidates, int *count, int *selected, pt_stream_t stream);
+
 /* Instruction-schedule variant of the MFMA kernels (tuning knob):
  * 0 = compiler default, 1 and 2 = iglp strategies (2 is the default),
  * 3 = MFMA / LDS-read interleave, 4 and 5 = two 256x128 workgroups per CU

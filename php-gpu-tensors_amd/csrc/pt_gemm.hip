@@ -27,6 +27,11 @@
 
 #include <string.h>
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <string>
+
 namespace pt {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -783,6 +788,17 @@ static const TileInfo kTiles[TILE_COUNT] = {
 
 static int g_tile_override = -1;
 
+// Tiles chosen by pt_matmul_tune, per (dtype, M, N, K, batch, layout).
+static std::mutex g_tuned_mu;
+static std::map<std::string, int> g_tuned;
+
+static std::string tune_key(int dtype, int M, int N, int K, long long batch, bool a_k1, bool b_k1)
+{
+    char key[96];
+    snprintf(key, sizeof(key), "%d:%d:%d:%d:%lld:%d:%d", dtype, M, N, K, batch, a_k1 ? 1 : 0, b_k1 ? 1 : 0);
+    return key;
+}
+
 // K step per LDS stage: 32 for 16-bit operands, 16 for fp32 (same bytes).
 template <int DT> struct GemmBK { static constexpr int v = DT == PT_FLOAT32 ? 16 : 32; };
 
@@ -850,15 +866,17 @@ pt_status pt_matmul_set_precision(int precision)
 {
     if (precision != 0 && precision != 1)
         return fail(PT_ERR_INVALID, "Unknown matmul precision %d", precision);
+    // gfx950 has no reduced-precision fp32 (xf32) MFMA: a TF32 request is
+    // refused as on a device without TF32, and strict fp32 stays selected
+    if (precision == 1)
+        return fail(PT_ERR_UNSUPPORTED, "TF32 matmul precision is not available on gfx950");
     g_precision = precision;
     return PT_OK;
 }
 
 const char *pt_matmul_precision_name(void)
 {
-    // gfx950 has no reduced-precision fp32 (xf32) MFMA: both requests run
-    // true fp32 products, and the name says so.
-    return g_precision == 0 ? "fp32-strict" : "fp32-strict (tf32 unavailable on gfx950)";
+    return "fp32-strict";
 }
 
 // Instruction-scheduling variant of the 256x256 kernels (tuning knob):
@@ -950,6 +968,16 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     if (!a_kc && !a_rc) a_kc = true;  // checked path handles arbitrary strides
     if (!b_kc && !b_rc) b_kc = true;
     int tile = g_tile_override;
+    bool tuned = false;
+    if (tile < 0) {
+        std::lock_guard<std::mutex> lock(g_tuned_mu);
+        auto it = g_tuned.find(tune_key(dtype, g.M, g.N, g.K, batch, g.a_sk == 1, g.b_sk == 1));
+        if (it != g_tuned.end()) {
+            tile = it->second;
+            tuned = true;
+        }
+    }
+    const char *suffix = tuned ? "-tuned" : "";
     if (tile < 0) {
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
@@ -987,7 +1015,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
             }
             PT_LAUNCH_CHECK("matmul");
             counters().mfma_gemm_calls++;
-            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s", "mfma-direct-lds");
+            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "mfma-direct-lds%s", suffix);
             return PT_OK;
         }
         tile = TILE_256x256;
@@ -1064,15 +1092,86 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         PT_TRY(check_hip(e1, "matmul (split-K partials)"));
         PT_TRY(check_hip(e2, "matmul (split-K sum)"));
         counters().mfma_gemm_calls++;
-        snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s",
-                 dtype == PT_FLOAT32 ? "mfma-fp32-splitk" : "mfma-low-precision-splitk");
+        snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s%s",
+                 dtype == PT_FLOAT32 ? "mfma-fp32-splitk" : "mfma-low-precision-splitk", suffix);
         return PT_OK;
     }
     PT_LAUNCH_CHECK("matmul");
     counters().mfma_gemm_calls++;
-    snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s",
-             dtype == PT_FLOAT32 ? "mfma-fp32" : "mfma-low-precision");
+    snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s%s",
+             dtype == PT_FLOAT32 ? "mfma-fp32" : "mfma-low-precision", suffix);
     return PT_OK;
+}
+
+pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
+                         const int *shape_a, const size_t *strides_a, int nd_a,
+                         const int *shape_b, const size_t *strides_b, int nd_b,
+                         const int *shape_c, int nd_c, int *tiles, float *median_ms,
+                         int max_candidates, int *count, int *selected, pt_stream_t stream)
+{
+    PT_TRY(ensure_init());
+    if (nd_a < 2 || nd_b < 2 || nd_c < 2 || !count || !selected)
+        return fail(PT_ERR_INVALID, "matmul tuning needs rank >= 2 operands and result slots");
+    const int M = shape_a[nd_a - 2], K = shape_a[nd_a - 1], N = shape_b[nd_b - 1];
+    // the reference tunes its cuBLASLt range only (1e7 <= M*N*K,
+    // matmul_kernels.cu:336-456)
+    if ((double)M * (double)N * (double)K < 1e7)
+        return fail(PT_ERR_INVALID, "matmul is too small for autotuning (M*N*K below 1e7)");
+    long long batch = 1;
+    for (int d = 0; d < nd_c - 2; d++) batch *= shape_c[d];
+    const bool a_k1 = strides_a[nd_a - 1] == 1, b_k1 = strides_b[nd_b - 2] == 1;
+    static const int kFp32[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
+                                TILE_256x128_W8, TILE_128x128_W8, TILE_128x128_W8_K2, TILE_128x64_W4M2,
+                                TILE_128x64_W4M2_K2};
+    static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
+                                TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8};
+    const int *cands = dtype == PT_FLOAT32 ? kFp32 : kHalf;
+    const int ncand = dtype == PT_FLOAT32 ? (int)(sizeof(kFp32) / sizeof(int)) : (int)(sizeof(kHalf) / sizeof(int));
+    hipStream_t s = stream_of(stream);
+    hipEvent_t e0, e1;
+    PT_TRY(check_hip(hipEventCreate(&e0), "tuning event"));
+    PT_TRY(check_hip(hipEventCreate(&e1), "tuning event"));
+    const int saved = g_tile_override;
+    pt_status st = PT_OK;
+    int n = 0, best = -1;
+    float best_ms = 0.0f;
+    for (int ci = 0; ci < ncand && st == PT_OK; ci++) {
+        g_tile_override = cands[ci];
+        st = pt_matmul(a, b, c, dtype, shape_a, strides_a, nd_a, shape_b, strides_b, nd_b, shape_c, nd_c, stream);
+        float times[5];
+        for (int r = 0; r < 5 && st == PT_OK; r++) {
+            st = check_hip(hipEventRecord(e0, s), "tuning event");
+            if (st == PT_OK)
+                st = pt_matmul(a, b, c, dtype, shape_a, strides_a, nd_a, shape_b, strides_b, nd_b, shape_c, nd_c,
+                               stream);
+            if (st == PT_OK) st = check_hip(hipEventRecord(e1, s), "tuning event");
+            if (st == PT_OK) st = check_hip(hipEventSynchronize(e1), "tuning wait");
+            if (st == PT_OK) st = check_hip(hipEventElapsedTime(&times[r], e0, e1), "tuning time");
+        }
+        if (st != PT_OK) break;
+        std::sort(times, times + 5);
+        if (n < max_candidates && tiles && median_ms) {
+            tiles[n] = cands[ci];
+            median_ms[n] = times[2];
+        }
+        if (best < 0 || times[2] < best_ms) {
+            best = n;
+            best_ms = times[2];
+        }
+        n++;
+    }
+    g_tile_override = saved;
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    PT_TRY(st);
+    *count = n < max_candidates ? n : max_candidates;
+    *selected = best;
+    {
+        std::lock_guard<std::mutex> lock(g_tuned_mu);
+        g_tuned[tune_key(dtype, M, N, K, batch, a_k1, b_k1)] = cands[best];
+    }
+    // the tuned choice runs once more, so `c` holds its product
+    return pt_matmul(a, b, c, dtype, shape_a, strides_a, nd_a, shape_b, strides_b, nd_b, shape_c, nd_c, stream);
 }
 
 }  // extern "C"

@@ -258,6 +258,13 @@ phpt_tensor *phpt_matmul(phpt_tensor *a, phpt_tensor *b)
     return wrap(cuda_tensor_matmul(a->t, b->t));
 }
 
+phpt_tensor *phpt_tune_matmul(phpt_tensor *a, phpt_tensor *b, int *tiles, float *median_ms,
+                              int max_candidates, int *count, int *selected)
+{
+    clear_error();
+    return wrap(cuda_tune_matmul(a->t, b->t, tiles, median_ms, max_candidates, count, selected));
+}
+
 phpt_tensor *phpt_where(phpt_tensor *c, phpt_tensor *x, phpt_tensor *y)
 {
     clear_error();

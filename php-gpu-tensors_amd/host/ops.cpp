@@ -515,6 +515,42 @@ TensorP cuda_tensor_matmul(const TensorP &a, const TensorP &b)
     return out;
 }
 
+// cuda_tune_matmul (matmul_kernels.h:34-38): a measured tile choice kept
+// for this problem by the device library; eager only
+TensorP cuda_tune_matmul(const TensorP &a, const TensorP &b, int *tiles, float *median_ms, int max_candidates,
+                         int *count, int *selected)
+{
+    if (!a || !b) {
+        set_invalid("Missing tensor operand");
+        return nullptr;
+    }
+    if (fusion_active()) {
+        set_runtime("matmul tuning cannot run inside a Fusion scope");
+        return nullptr;
+    }
+    if (a->dtype != b->dtype ||
+        (a->dtype != PT_FLOAT32 && a->dtype != PT_FLOAT16 && a->dtype != PT_BFLOAT16)) {
+        set_invalid("matmul requires matching float32, float16 or bfloat16 operands");
+        return nullptr;
+    }
+    int shape[kMaxDims], nd;
+    if (!matmul_shape(a->shape, a->ndims, b->shape, b->ndims, shape, &nd)) {
+        set_invalid("matmul requires rank >= 2, matching inner dimensions and broadcast-compatible batches");
+        return nullptr;
+    }
+    if (!guard(a) || !guard(b)) return nullptr;
+    TensorP out = output_tensor(shape, nd, a->dtype);
+    if (!out) return nullptr;
+    const char *pa = (const char *)base_ptr(a) + a->offset * dtype_size(a->dtype);
+    const char *pb = (const char *)base_ptr(b) + b->offset * dtype_size(b->dtype);
+    if (!check_status(pt_matmul_tune(pa, pb, out->storage->ptr, a->dtype, a->shape, a->strides, a->ndims,
+                                     b->shape, b->strides, b->ndims, shape, nd, tiles, median_ms, max_candidates,
+                                     count, selected, nullptr),
+                      "Matmul tuning failed"))
+        return nullptr;
+    return out;
+}
+
 // ------------------------------------------------------- native dispatcher
 TensorP native_execute(const NativeSpec &sp, const std::vector<TensorP> &in)
 {

@@ -66,6 +66,11 @@ phpt_tensor *phpt_softmax(phpt_tensor *a, int axis);
 phpt_tensor *phpt_layernorm(phpt_tensor *a, const int *axes, int naxes, double eps,
                             phpt_tensor *scale, phpt_tensor *bias);
 phpt_tensor *phpt_matmul(phpt_tensor *a, phpt_tensor *b);
+/* cuda_tune_matmul: times every tile configuration for a @ b, keeps the
+ * fastest for that problem and returns the product; tiles / median_ms get up
+ * to max_candidates entries.  NULL on error (too small: invalid argument). */
+phpt_tensor *phpt_tune_matmul(phpt_tensor *a, phpt_tensor *b, int *tiles, float *median_ms,
+                              int max_candidates, int *count, int *selected);
 phpt_tensor *phpt_where(phpt_tensor *c, phpt_tensor *x, phpt_tensor *y);
 phpt_tensor *phpt_astype(phpt_tensor *a, int dtype);
 phpt_tensor *phpt_copy(phpt_tensor *a);

@@ -136,6 +136,8 @@ TensorP cuda_array_softmax(const TensorP &a, int axis);
 TensorP cuda_array_layernorm(const TensorP &a, const int *axes, int naxes, double eps,
                              const TensorP &scale, const TensorP &bias);
 TensorP cuda_tensor_matmul(const TensorP &a, const TensorP &b);
+TensorP cuda_tune_matmul(const TensorP &a, const TensorP &b, int *tiles, float *median_ms, int max_candidates,
+                         int *count, int *selected);
 TensorP cuda_tensor_where(const TensorP &c, const TensorP &x, const TensorP &y);
 TensorP tensor_cast(const TensorP &a, int dtype);
 TensorP astype(const TensorP &a, int dtype);  // safe casts only (CudaArray::astype)

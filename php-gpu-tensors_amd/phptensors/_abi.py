@@ -110,6 +110,9 @@ SIGNATURES = {
                                     ctypes.c_size_t, ctypes.c_double, vp, vp, vp]),
     "pt_matmul": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, c_int_p, c_size_p, ctypes.c_int,
                                  c_int_p, c_size_p, ctypes.c_int, c_int_p, ctypes.c_int, vp]),
+    "pt_matmul_tune": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, c_int_p, c_size_p, ctypes.c_int,
+                                      c_int_p, c_size_p, ctypes.c_int, c_int_p, ctypes.c_int, c_int_p,
+                                      ctypes.POINTER(ctypes.c_float), ctypes.c_int, c_int_p, c_int_p, vp]),
     "pt_matmul_set_precision": (ctypes.c_int, [ctypes.c_int]),
     "pt_matmul_precision_name": (ctypes.c_char_p, []),
     "pt_matmul_set_tile": (ctypes.c_int, [ctypes.c_int]),

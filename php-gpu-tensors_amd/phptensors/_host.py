@@ -45,6 +45,8 @@ SIGNATURES = {
     "phpt_softmax": (T, [T, ctypes.c_int]),
     "phpt_layernorm": (T, [T, ip, ctypes.c_int, ctypes.c_double, T, T]),
     "phpt_matmul": (T, [T, T]),
+    "phpt_tune_matmul": (T, [T, T, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float), ctypes.c_int,
+                             ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "phpt_where": (T, [T, T, T]),
     "phpt_astype": (T, [T, ctypes.c_int]),
     "phpt_copy": (T, [T]),

@@ -273,3 +273,61 @@ def test_config4_full_size_sampled(A, dt):
             assert abs(g - exact) <= 1e-4 * math.sqrt(k) * scale
         else:
             assert abs(g - exact) <= 1e-2 * max(abs(exact), scale / math.sqrt(k))
+
+
+# ------------------------------------------------ precision policy and tuning
+def test_matmul_precision_reference():
+    """matmul_precision.phpt:14-57 on a device without TF32: strict fp32 is the
+    default, an unknown mode is refused without changing it, and a TF32
+    request raises RuntimeException (gfx950 has no xf32 MFMA)."""
+    from phptensors import backend as B
+    from phptensors import InvalidArgumentException, RuntimeException
+    assert B.cuda_get_backend_info()["precision"] == "fp32-strict"
+    with pytest.raises(InvalidArgumentException):
+        B.cuda_set_matmul_precision("unknown")
+    assert B.cuda_get_backend_info()["precision"] == "fp32-strict"
+    with pytest.raises(RuntimeException):
+        B.cuda_set_matmul_precision("tf32")
+    assert B.cuda_get_backend_info()["precision"] == "fp32-strict"
+    B.cuda_set_matmul_precision("fp32-strict")
+
+
+def test_matmul_tuning_reference():
+    """matmul_tuning.phpt:12-46: tuning a 256x256 product measures candidates,
+    selects exactly one, later products of that shape use it and stay exact,
+    and a 32x32 product is not eligible."""
+    from phptensors import backend as B
+    from phptensors import CudaArray, InvalidArgumentException
+    left, right = CudaArray.ones([256, 256]), CudaArray.ones([256, 256])
+    tuning = B.cuda_tune_matmul(left, right)
+    assert tuning["precision"] == "fp32-strict"
+    assert tuning["candidateCount"] > 0
+    assert 0 <= tuning["selectedCandidate"] < tuning["candidateCount"]
+    selected = 0
+    for i, cand in enumerate(tuning["candidates"]):
+        assert cand["workspaceBytes"] == 0
+        assert np.isfinite(cand["medianMs"]) and cand["medianMs"] > 0
+        if cand["selected"]:
+            assert i == tuning["selectedCandidate"]
+            selected += 1
+    assert selected == 1
+    assert np.all(tuning["product"].toNumpy() == 256.0)
+    product = left.matmul(right).toNumpy()
+    assert product.shape == (256, 256) and np.all(product == 256.0)
+    assert B.cuda_get_backend_info()["lastMatmul"].endswith("-tuned")
+    with pytest.raises(InvalidArgumentException):
+        B.cuda_tune_matmul(CudaArray.ones([32, 32]), CudaArray.ones([32, 32]))
+    # a tuned choice applies to its own shape only
+    other = CudaArray.ones([256, 128]).matmul(CudaArray.ones([128, 256]))
+    assert np.all(other.toNumpy() == 128.0)
+    assert not B.cuda_get_backend_info()["lastMatmul"].endswith("-tuned")
+
+
+def test_matmul_large_dispatch_reference():
+    """matmul_large_dispatch.phpt: a 4096x4096 fp32 product of ones is exact
+    (4096 everywhere) and runs the large-problem MFMA kernel."""
+    from phptensors import backend as B
+    from phptensors import CudaArray
+    out = CudaArray.ones([4096, 4096]).matmul(CudaArray.ones([4096, 4096])).toNumpy()
+    assert np.all(out == 4096.0)
+    assert B.cuda_get_backend_info()["lastMatmul"] == "mfma-fp32"
