@@ -139,6 +139,40 @@ def _unary_backward(op, x, out):
     return None
 
 
+def _bound(text):
+    text = text.strip()
+    return None if text == "" else int(text)
+
+
+def _parse_selector(text):
+    """One selector of a slice() expression: "i", ":", "a:b", "a:b:c"."""
+    text = text.strip()
+    if ":" not in text:
+        if text == "":
+            raise InvalidArgumentException("slice() selector is empty")
+        return ("index", int(text))
+    parts = text.split(":")
+    if len(parts) > 3:
+        raise InvalidArgumentException(f"slice() selector '{text}' has too many ':'")
+    parts += [""] * (3 - len(parts))
+    return ("range", tuple(_bound(p) for p in parts))
+
+
+def _selector(sel):
+    if sel is None:
+        return ("range", (None, None, None))
+    if isinstance(sel, (bool, np.bool_)):
+        raise InvalidArgumentException("slice() selectors cannot be booleans")
+    if isinstance(sel, (int, np.integer)):
+        return ("index", int(sel))
+    if isinstance(sel, (list, tuple)):
+        if not 1 <= len(sel) <= 3:
+            raise InvalidArgumentException("slice() ranges are [start, stop] or [start, stop, step]")
+        vals = [None if v is None else int(v) for v in sel] + [None] * (3 - len(sel))
+        return ("range", tuple(vals))
+    raise InvalidArgumentException(f"Unsupported slice() selector {sel!r}")
+
+
 class CudaArray:
     """GPU tensor handle (src/tensor.h tensor_t behind a CudaArray object)."""
 
@@ -283,7 +317,10 @@ class CudaArray:
         return bits
 
     def toArray(self):
-        return self.toNumpy().tolist()
+        """Nested lists; a rank-0 tensor exports as a one-element list, as the
+        reference's toArray() does (tests/slice.phpt:22-24)."""
+        values = self.toNumpy().tolist()
+        return [values] if self.getNdims() == 0 else values
 
     def toBuffer(self):
         """Raw element bytes, row-major (cuda_array_ce.c:2943-2951)."""
@@ -526,7 +563,44 @@ class CudaArray:
             AG.record(out, [self], lambda g: [AG.reduce_to(g, src)], "broadcast")
         return out
 
-    def slice(self, axis, start, stop, step=1):
+    def slice(self, *selectors):
+        """CudaArray::slice(int|string|array|null ...$selectors)
+        (stubs/cuda.stub.php:441-444): a view with one selector per leading
+        axis.  An int is an index and drops its axis; [start, stop(, step)]
+        or "start:stop:step" is an exclusive-stop range with a positive step
+        (negative bounds count from the end, bounds clip to the axis, empty
+        parts take their defaults); None or ":" keeps the axis whole; a
+        string may hold several comma-separated selectors."""
+        parsed = []
+        for sel in selectors:
+            if isinstance(sel, str):
+                parsed.extend(_parse_selector(part) for part in sel.split(","))
+            else:
+                parsed.append(_selector(sel))
+        if len(parsed) > self.getNdims():
+            raise InvalidArgumentException(
+                f"slice() got {len(parsed)} selectors for a tensor of rank {self.getNdims()}")
+        out, axis = self, 0
+        for kind, value in parsed:
+            if kind == "index":
+                out = out.select(axis, value)
+                continue
+            start, stop, step = value
+            n = out.getShape()[axis]
+            start = 0 if start is None else start
+            stop = n if stop is None else stop
+            step = 1 if step is None else step
+            if step <= 0:
+                raise InvalidArgumentException("slice() steps must be positive")
+            start = max(-n, min(start, n))
+            stop = max(-n, min(stop, n))
+            out = out._slice_axis(axis, start, stop, step)
+            axis += 1
+        if out is self:  # no selectors: the whole tensor as a view
+            out = CudaArray._wrap(_host.load().phpt_retain(self._h))
+        return out
+
+    def _slice_axis(self, axis, start, stop, step=1):
         return CudaArray._wrap(_host.load().phpt_slice(self._h, int(axis), int(start), int(stop), int(step)))
 
     def select(self, axis, index):
@@ -639,6 +713,19 @@ def _record_scalar(out, a, s, op, reverse):
         back = lambda g: [g * s]  # noqa: E731
     elif op == OP["DIV"]:
         back = (lambda g: [-(g * s) / (a * a)]) if reverse else (lambda g: [g / s])  # noqa: E731
+    elif op == OP["POW"] and not reverse:
+        # x ** s: g * (x ** (s - 1) * s); zero for s == 0 (autograd.c:1256-1280)
+        if float(s) == 0.0:
+            back = lambda g: [g * 0.0]  # noqa: E731
+        else:
+            back = lambda g: [g * ((a.astype(g.getDtype()) ** (float(s) - 1.0)) * s)]  # noqa: E731
+    elif op in (OP["MAXIMUM"], OP["MINIMUM"]):
+        # the tensor side takes the gradient where it wins, half of it at a
+        # tie with the scalar (autograd.c:1282-1296)
+        def back(g):
+            wins = a.ge(s) if op == OP["MAXIMUM"] else a.le(s)
+            zeros = g * 0.0
+            return [CudaArray.where(a.eq(s), g * 0.5, CudaArray.where(wins, g, zeros))]
     elif op in (OP["GT"], OP["LT"], OP["EQ"], OP["NE"], OP["GE"], OP["LE"]):
         return
     else:

@@ -261,7 +261,7 @@ def test_scalar_exports(dtype):
     assert tensor.toArray() == expected
     assert tensor.select(0, 0).item() == expected[0] and tensor.select(0, 1).item() == expected[1]
     assert type(tensor.select(0, 0).item()) is type(expected[0])
-    assert tensor.slice(0, 1, 2).reshape([1]).item() == expected[1]
+    assert tensor.slice("1:2").reshape([1]).item() == expected[1]
     strided = A(np.array([expected, expected], npdt) if npdt else [expected, expected], dtype).transpose()
     assert strided.select(0, 1).select(0, 1).item() == expected[1]
 
@@ -272,7 +272,7 @@ def test_uint64_exports():
     data = struct.pack("<3Q", 2**63 - 1, 2**63, 2**64 - 1)
     want = [2**63 - 1, 2**63, 2**64 - 1]
     unsigned = A.fromBuffer(data, [3], "uint64")
-    for tensor in (unsigned, unsigned.copy(), F.run(lambda: unsigned.slice(0, 0, 3))):
+    for tensor in (unsigned, unsigned.copy(), F.run(lambda: unsigned.slice())):
         assert tensor.toArray() == want
         for i, v in enumerate(want):
             assert tensor.select(0, i).item() == v
@@ -474,3 +474,34 @@ def test_low_precision_gradient_in_compiled_plan(dtype):
     plain = F.compile(lambda x: x.sum(), [A.fromFlatArray([1.0, 2.0, 3.0], [3], dtype)])
     with pytest.raises(InvalidArgumentException):
         plain.run(tracked)
+
+
+def test_extended_operations_reference():
+    """cudaarray_extended.phpt:9-25, 31-38, 95-97 and its expected lines 1-12,
+    15-18, 25 and 27 (gather / scatterAdd are indexed operations outside this
+    build's path and are left out)."""
+    x = A([[1.0, 0.0], [3.0, 4.0]])
+    assert x.maximum(0).toArray() == [[1, 0], [3, 4]]
+    assert x.minimum(0).toArray() == [[0, 0], [0, 0]]
+    assert x.clamp(0, 2).toArray() == [[1, 0], [2, 2]]
+    assert x.all(1).toArray() == [False, True] and x.any(1).toArray() == [True, True]
+    assert "%.3f %.3f" % (x.var().item(), x.std().item()) == "2.500 1.581"
+    assert x.var(0).toArray() == [1, 4]
+    assert A([[7.0], [8.0]]).squeeze(1).getShape() == [2]
+    assert x.unsqueeze(1).getShape() == [2, 1, 2]
+    assert A([[1.0, 2.0]]).broadcastTo([2, 2]).toArray() == [[1, 2], [1, 2]]
+    assert A([[1.0, 2.0], [3.0, 4.0]]).transpose().unsqueeze(0).squeeze(0).toArray() == [[1, 3], [2, 4]]
+    item = A.full([1], 42, "int64").item()
+    assert item == 42 and isinstance(item, int)
+    graph = F.compile(lambda t: t.clamp(0, 2).maximum(0.5).var(), [x])
+    assert "%.3f" % graph.run(x).item() == "0.422"
+    logical = F.compile(lambda t: [t.all(1), t.any(1)], [x])
+    all_, any_ = logical.run(x)
+    assert all_.toArray() == [False, True] and any_.toArray() == [True, True]
+    broadcast = F.compile(lambda t: t.broadcastTo([2, 2]).sum(0), [A([1.0, 2.0])])
+    assert broadcast.run(A([1.0, 2.0])).toArray() == [2, 4]
+    with pytest.raises(InvalidArgumentException):
+        x.var(1, 2)
+    tracked = A([-1.0, 0.5, 3.0]).requiresGrad()
+    tracked.clamp(0, 2).sum().backward()
+    assert tracked.grad().toArray() == [0, 1, 0]
