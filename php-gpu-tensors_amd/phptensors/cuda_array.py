@@ -139,6 +139,24 @@ def _unary_backward(op, x, out):
     return None
 
 
+def _nested_array(data):
+    """Nested lists of numbers (or a numpy array) as a rectangular numeric
+    array of rank at most 10; ragged, non-numeric or deeper input raises
+    InvalidArgumentException, as the reference's constructor does."""
+    if isinstance(data, np.ndarray):
+        arr = data
+    else:
+        try:
+            arr = np.asarray(data)
+        except (ValueError, TypeError) as exc:
+            raise InvalidArgumentException(f"CudaArray input must be a rectangular numeric array: {exc}")
+    if arr.dtype.kind not in "biuf":
+        raise InvalidArgumentException("CudaArray input must hold numbers or booleans only")
+    if arr.ndim > 10:
+        raise InvalidArgumentException("CudaArray input is nested deeper than 10 dimensions")
+    return arr
+
+
 def _bound(text):
     text = text.strip()
     return None if text == "" else int(text)
@@ -185,9 +203,7 @@ class CudaArray:
         self._grad = None
         if data is None:
             return
-        arr = np.asarray(data)
-        h = _from_numpy(arr, dtype_code(dtype))
-        self._h = h
+        self._h = _from_numpy(_nested_array(data), dtype_code(dtype))
 
     @classmethod
     def _wrap(cls, handle, what=""):
@@ -219,7 +235,16 @@ class CudaArray:
 
     @classmethod
     def fromFlatArray(cls, values, shape, dtype="float32"):
-        return cls.fromNumpy(np.asarray(values).reshape(shape), dtype)
+        """A flat list of numbers laid out in `shape` (non-negative extents
+        whose product is the list's length)."""
+        arr = _nested_array(values)
+        if arr.ndim > 1:
+            raise InvalidArgumentException("fromFlatArray() expects a flat list of values")
+        shape = [int(d) for d in shape]
+        if any(d < 0 for d in shape) or int(np.prod(shape, dtype=object)) != arr.size:
+            raise InvalidArgumentException(
+                f"fromFlatArray() shape {shape} does not hold {arr.size} values")
+        return cls.fromNumpy(arr.reshape(shape), dtype)
 
     @classmethod
     def fromBuffer(cls, data, shape, dtype="float32"):
