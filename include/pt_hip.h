@@ -127,6 +127,11 @@ pt_status pt_stream_synchronize(pt_stream_t stream);
 pt_status pt_stream_query(pt_stream_t stream, int *finished);
 pt_status pt_stream_wait_event(pt_stream_t stream, pt_event_t event);
 pt_stream_t pt_default_stream(void);
+/* Stream used on the calling thread by calls that pass a NULL stream (the
+ * runtime stream when `stream` is NULL).  Lets a host runtime route whole
+ * operations to the branches of a multi-stream graph capture; replaces the
+ * plan stream of fusion_enqueue (fusion_execute.c:385-412). */
+pt_status pt_stream_set_current(pt_stream_t stream);
 pt_status pt_event_create(pt_event_t *event);
 pt_status pt_event_destroy(pt_event_t event);
 pt_status pt_event_record(pt_event_t event, pt_stream_t stream);
@@ -350,9 +355,11 @@ pt_status pt_launch(pt_function_t function, unsigned grid_x, unsigned block_x,
  * multi-kernel operations (split-K partials, column and global reduction
  * partials) is carved from [base, base + bytes) instead of the stream-
  * ordered pool, so a captured graph holds no allocation; an operation whose
- * scratch does not fit fails with PT_ERR_NOMEM.  base NULL and bytes 0:
- * measuring mode (pool allocations, peak recorded).  end reports the peak
- * scratch bytes held at once (256-byte granules). */
+ * scratch does not fit fails with PT_ERR_NOMEM.  A region is not handed
+ * out again before end, so operations that run concurrently (branches of a
+ * captured graph) never share scratch.  base NULL and bytes 0: measuring
+ * mode (pool allocations, total recorded).  end reports the scratch bytes
+ * taken between begin and end (256-byte granules). */
 pt_status pt_workspace_begin(void *base, size_t bytes);
 pt_status pt_workspace_end(size_t *peak_bytes);
 

@@ -90,9 +90,13 @@ pt_status ensure_init()
     return g_init_status;
 }
 
+// Stream that calls without an explicit stream use on this thread: the
+// runtime stream unless pt_stream_set_current chose another.
+static thread_local hipStream_t t_current = nullptr;
+
 hipStream_t stream_of(pt_stream_t s)
 {
-    return s ? (hipStream_t)s : g_stream;
+    return s ? (hipStream_t)s : (t_current ? t_current : g_stream);
 }
 
 // Scratch of the multi-kernel operations (split-K partials, column and
@@ -139,13 +143,10 @@ void scratch_free(void *ptr, hipStream_t stream)
     for (size_t i = t_ws.stack.size(); i-- > 0;) {
         if (t_ws.stack[i].first != ptr) continue;
         if (t_ws.measure) (void)hipFreeAsync(ptr, stream);
+        // the region is not handed out again before pt_workspace_end, so
+        // operations that run concurrently (branches of a captured graph)
+        // never share scratch
         t_ws.stack.erase(t_ws.stack.begin() + (long)i);
-        // held bytes: the end of the highest live entry in the arena, the
-        // sum of the live entries when measuring
-        t_ws.top = 0;
-        for (auto &e : t_ws.stack)
-            t_ws.top = t_ws.measure ? t_ws.top + e.second
-                                    : std::max(t_ws.top, (size_t)((char *)e.first - t_ws.base) + e.second);
         return;
     }
 }
@@ -520,6 +521,12 @@ pt_status pt_workspace_end(size_t *peak_bytes)
     const bool leaked = !t_ws.stack.empty();
     t_ws = Workspace();
     if (leaked) return fail(PT_ERR_RUNTIME, "scratch still held at the end of the workspace");
+    return PT_OK;
+}
+
+pt_status pt_stream_set_current(pt_stream_t stream)
+{
+    t_current = (hipStream_t)stream;
     return PT_OK;
 }
 

@@ -1345,6 +1345,114 @@ static bool run_steps(Plan &p, std::vector<TensorP> &vals)
     return true;
 }
 
+// Graph capture over several streams.  Each step runs on a branch: the
+// branch of its latest dependency when that branch has not moved on, else
+// the least recently used branch, after waiting on the events of the steps
+// it reads that ran on other branches.  Independent steps (the weight and
+// input gradients of one layer, a bias-gradient reduction beside a GEMM,
+// the optimizer update of one layer beside the next layer's products) then
+// become parallel branches of the captured graph, as the reference's plan
+// stream orders native and fused steps (fusion_execute.c:385-412); the
+// values and the order of every dependency are unchanged.
+static constexpr int kBranches = 3;
+
+static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<pt_event_t> &events)
+{
+    const int ns = (int)p.steps.size();
+    std::vector<int> producer(p.items.size(), -1);
+    for (int i = 0; i < ns; i++) {
+        const Step &st = p.steps[i];
+        if (st.native) producer[st.item] = i;
+        else
+            for (int r : p.kernels[st.kernel].roots) producer[r] = i;
+    }
+    auto source = [&](int id) {
+        // an uncut view chain handed to a native reads the item it views
+        while (p.items[id].kind == IT_ELEM && !p.items[id].cut && p.items[id].t->node->kind == N_VIEW)
+            id = p.items[id].args[0];
+        return id;
+    };
+    static thread_local std::vector<pt_stream_t> side;
+    while ((int)side.size() < kBranches - 1) {
+        pt_stream_t s = nullptr;
+        if (!check_status(pt_stream_create(&s), "Fusion branch stream")) return false;
+        side.push_back(s);
+    }
+    std::vector<pt_stream_t> streams = {pt_default_stream()};
+    for (pt_stream_t s : side) streams.push_back(s);
+    auto new_event = [&](pt_event_t &e) {
+        if (!check_status(pt_event_create(&e), "Fusion branch event")) return false;
+        events.push_back(e);
+        return true;
+    };
+    bool ok = true;
+    pt_event_t fork = nullptr;
+    ok = new_event(fork) && check_status(pt_event_record(fork, streams[0]), "Fusion branch fork");
+    std::vector<int> branch(ns, 0), last(kBranches, -1);
+    std::vector<char> joined(kBranches, 0);
+    joined[0] = 1;
+    std::vector<pt_event_t> done(ns, nullptr);
+    for (int i = 0; i < ns && ok; i++) {
+        const Step &st = p.steps[i];
+        std::vector<int> deps;
+        if (st.native) {
+            for (int a : p.items[st.item].args) deps.push_back(producer[source(a)]);
+        } else {
+            for (int l : p.kernels[st.kernel].leaves) deps.push_back(producer[l]);
+        }
+        deps.erase(std::remove(deps.begin(), deps.end(), -1), deps.end());
+        int latest = deps.empty() ? -1 : *std::max_element(deps.begin(), deps.end());
+        int b = -1;
+        if (latest >= 0 && last[branch[latest]] == latest) b = branch[latest];
+        if (b < 0) {
+            b = 0;
+            for (int c = 1; c < kBranches; c++)
+                if (last[c] < last[b]) b = c;
+        }
+        if (!joined[b]) {
+            ok = check_status(pt_stream_wait_event(streams[b], fork), "Fusion branch join");
+            joined[b] = 1;
+        }
+        for (int d : deps)
+            if (ok && branch[d] != b) ok = check_status(pt_stream_wait_event(streams[b], done[d]), "Fusion branch wait");
+        if (!ok) break;
+        branch[i] = b;
+        last[b] = i;
+        pt_stream_set_current(streams[b]);
+        if (st.native) {
+            Item &it = p.items[st.item];
+            std::vector<TensorP> ins;
+            for (int a : it.args) {
+                TensorP v = native_arg(p, vals, a);
+                if (!v) {
+                    ok = false;
+                    break;
+                }
+                ins.push_back(v);
+            }
+            if (ok) {
+                preset_output(vals[st.item]);
+                TensorP out = native_execute(it.t->node->native, ins);
+                preset_output(nullptr);
+                if (!out) ok = false;
+                else vals[st.item] = out;
+            }
+        } else {
+            ok = launch_kernel(p, p.kernels[st.kernel], vals);
+        }
+        pt_stream_set_current(nullptr);
+        if (ok) ok = new_event(done[i]) && check_status(pt_event_record(done[i], streams[b]), "Fusion branch event");
+    }
+    // every branch joins the capture stream again before the capture ends
+    for (int b = 1; b < kBranches && ok; b++) {
+        if (!joined[b]) continue;
+        pt_event_t e = nullptr;
+        ok = new_event(e) && check_status(pt_event_record(e, streams[b]), "Fusion branch end") &&
+             check_status(pt_stream_wait_event(streams[0], e), "Fusion branch end");
+    }
+    return ok;
+}
+
 // Allocate materialized values for a run (outside graph capture): kernel
 // roots and the outputs of native steps.
 static bool prepare_values(Plan &p, std::vector<TensorP> &vals)
@@ -1398,15 +1506,25 @@ static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, boo
     captured = false;
     if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
     bool ok = true;
+    // branch events stay alive until the capture has ended
+    std::vector<pt_event_t> events;
+    struct Release {
+        std::vector<pt_event_t> &e;
+        ~Release()
+        {
+            for (pt_event_t x : e) pt_event_destroy(x);
+        }
+    } release{events};
     if (natives)
         ok = check_status(pt_workspace_begin(p.workspace->ptr, p.workspace_bytes), "Workspace setup failed");
     if (ok) {
         allocation_forbidden() = natives;
-        ok = run_steps(p, vals);
+        ok = run_steps_branched(p, vals, events);
         allocation_forbidden() = false;
         if (natives && !check_status(pt_workspace_end(nullptr), "Workspace release failed")) ok = false;
     }
     if (!ok) {
+        pt_stream_set_current(nullptr);
         pt_graph_t scrap = nullptr;
         if (pt_graph_end_capture(nullptr, &scrap) == PT_OK && scrap) pt_graph_destroy(scrap);
         p.graph_compatible = false;

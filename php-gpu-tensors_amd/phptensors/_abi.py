@@ -81,6 +81,7 @@ SIGNATURES = {
     "pt_stream_query": (ctypes.c_int, [vp, c_int_p]),
     "pt_stream_wait_event": (ctypes.c_int, [vp, vp]),
     "pt_default_stream": (vp, []),
+    "pt_stream_set_current": (ctypes.c_int, [vp]),
     "pt_event_create": (ctypes.c_int, [ctypes.POINTER(vp)]),
     "pt_event_destroy": (ctypes.c_int, [vp]),
     "pt_event_record": (ctypes.c_int, [vp, vp]),
