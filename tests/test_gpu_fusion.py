@@ -602,3 +602,34 @@ def test_power_reference_expectations(dtype):
     for low in ("float16", "bfloat16"):
         v = CudaArray.fromFlatArray([1.5, 2.0, 3.0], [3], low)
         assert Fusion.compile(lambda x: (x ** 2) + x, [v]).run(v).toBuffer() == ((v ** 2) + v).toBuffer()
+
+
+def test_graph_branches_replay_bitwise_like_eager():
+    """A captured plan whose independent steps run as parallel graph branches
+    (two GEMMs, their reductions, a fused update reading both, and an
+    unrelated elementwise chain) gives the eager results bit for bit on
+    every replay, with eager work between replays."""
+    r = np.random.default_rng(77)
+    x = CudaArray.fromNumpy(r.standard_normal((512, 256)).astype(np.float32))
+    w1 = CudaArray.fromNumpy(r.standard_normal((256, 384)).astype(np.float32))
+    w2 = CudaArray.fromNumpy(r.standard_normal((256, 128)).astype(np.float32))
+    z = CudaArray.fromNumpy(r.standard_normal((1000, 33)).astype(np.float32))
+
+    def body(x, w1, w2, z):
+        h1 = x.matmul(w1)
+        h2 = x.matmul(w2)
+        s1 = h1.sum(0)
+        m2 = h2.max(1)
+        g1 = x.transpose().matmul(h1)
+        upd = w1 - g1 * 0.001
+        chain = ((z * 2.0 + 1.0).tanh() * z).sum(1)
+        return [s1, m2, upd, chain, h2.mean()]
+
+    graph = Fusion.compile(body, [x, w1, w2, z], cudaGraph=True)
+    eager = [t.toBits() for t in body(x, w1, w2, z)]
+    for rep in range(5):
+        outs = graph.run(x, w1, w2, z)
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert np.array_equal(o.toBits(), e), (rep, i)
+        (x * 3.0).sum().toNumpy()  # eager work between replays
+    assert graph.getStats()["graphLaunches"] >= 3
