@@ -17,7 +17,9 @@ enough replicas to exceed the 256 MB Infinity Cache so that every launch
 streams from HBM.
 
 Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one
-GPU (the design note on sharding is in DESIGN.md).
+GPU.  Every workload here shards without exchange (batch of the GEMM, rows
+of the reductions and of the fused plan); the MLP step would shard its batch
+with one gradient all-reduce per step.
 """
 import argparse
 import ctypes
@@ -448,7 +450,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py runs on one GPU only: this build has no multi-GPU path "
-              "(DESIGN.md describes how the hot path would shard).", file=sys.stderr)
+              "(each workload would shard by batch or rows on one process per GPU).", file=sys.stderr)
         sys.exit(2)
     if os.environ.get("RANK", "0") != "0":
         return
