@@ -77,8 +77,20 @@ def _scalar_args(value):
     raise InvalidArgumentException(f"Unsupported scalar operand of type {type(value).__name__}")
 
 
+INT32_MIN, INT32_MAX = -2**31, 2**31 - 1
+
+
+def _int32(v, what="value"):
+    """An extent, index or axis for the C boundary: values outside int32 are
+    refused rather than narrowed (tests/cuda_shape_boundaries.phpt:23-36)."""
+    v = int(v)
+    if not INT32_MIN <= v <= INT32_MAX:
+        raise InvalidArgumentException(f"{what} {v} is out of range")
+    return v
+
+
 def _ints(seq):
-    seq = [int(v) for v in seq]
+    seq = [_int32(v, "dimension") for v in seq]
     return (ctypes.c_int * max(1, len(seq)))(*seq), len(seq)
 
 
@@ -486,7 +498,7 @@ class CudaArray:
     # ------------------------------------------------------------ reductions
     @staticmethod
     def _axis(axis):
-        return GLOBAL_AXIS if axis is None else int(axis)
+        return GLOBAL_AXIS if axis is None else _int32(axis, "axis")
 
     def _reduce(self, axis, op):
         out = CudaArray._wrap(_host.load().phpt_reduce(self._h, self._axis(axis), op))
@@ -559,7 +571,9 @@ class CudaArray:
 
     def transpose(self, axis=None):
         nd = self.getNdims()
-        perm = list(range(nd))[::-1] if axis is None else [a % nd for a in axis]
+        if axis is not None and any(not -nd <= int(a) < nd for a in axis):
+            raise InvalidArgumentException(f"transpose() axes {list(axis)} are out of range for rank {nd}")
+        perm = list(range(nd))[::-1] if axis is None else [int(a) % nd for a in axis]
         p, n = _ints(perm)
         out = CudaArray._wrap(_host.load().phpt_transpose(self._h, p, n))
         if AG.active(self):
@@ -629,7 +643,7 @@ class CudaArray:
         return CudaArray._wrap(_host.load().phpt_slice(self._h, int(axis), int(start), int(stop), int(step)))
 
     def select(self, axis, index):
-        return CudaArray._wrap(_host.load().phpt_select(self._h, int(axis), int(index)))
+        return CudaArray._wrap(_host.load().phpt_select(self._h, _int32(axis, "axis"), _int32(index, "index")))
 
     def unsqueeze(self, axis):
         shape = self.getShape()
