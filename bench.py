@@ -51,6 +51,9 @@ PMC_TRAFFIC_BYTES = {
     "gemm:bf16": 1_087_413_760, "gemm:fp16": 1_079_442_176, "gemm:fp32": 2_684_529_792,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
+# pt_backend_info last_matmul path -> kernel symbol
+GEMM_KERNELS = {"mfma-lds-ring": "k_gemm_ring", "mfma-direct-lds": "k_gemm_direct", "mfma-fp32": "k_gemm",
+                "mfma-low-precision": "k_gemm"}
 MALL_BYTES = 256 << 20
 
 
@@ -194,7 +197,7 @@ def fused_family(steps, warmup, replays=100):
     log(f"fused tanh(x+y*z): {ms * 1e3:.1f} us/replay  {gbs:.0f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM;"
         f" run() incl. bind+sync {run_ms * 1e3:.1f} us")
     res = {"ms": ms, "bytes": bytes_per, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS, "kernel": "fk0_v",
-           "run_ms_with_sync": run_ms, "replays_per_sample": replays}
+           "run_ms_with_sync": run_ms, "replays_per_sample": replays, "launches": replays}
     return {"workload": "config3: Fusion tanh(x + y*z), x,z [16384,8192] U(-2,2) seeds 3/31, "
                         "y [8192] seed 32; compiled once, replayed 100x via hipGraph",
             "ms_per_step": ms * replays, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS,
@@ -303,9 +306,11 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
         t.run(max(1, warmup))
         ms = t.run(max(1, steps))
         t.close()
+        path = A.backend_info().last_matmul.decode()
         tf = flops / (ms * 1e-3) / 1e12
         results[name] = {"ms": ms, "flop": flops, "TFLOP/s": tf, "peak": PEAK_TFLOPS[name],
-                         "frac": tf / PEAK_TFLOPS[name], "kernel": "k_gemm"}
+                         "frac": tf / PEAK_TFLOPS[name], "kernel": GEMM_KERNELS.get(path, "k_gemm"),
+                         "path": path}
         log(f"gemm {name}: {ms * 1e3:.1f} us  {tf:.1f} TFLOP/s  {100 * tf / PEAK_TFLOPS[name]:.1f}% of peak")
         del da, db, dc
     fam = {"workload": "config4: A,B [32,2048,2048] N(0,0.02) seeds 4/5; batched matmul "
@@ -482,11 +487,12 @@ def main():
         extra["eager"] = eager_family(args.steps, args.warmup)
     wall = time.perf_counter() - t_wall
 
-    # dominant kernel (largest time in a step) for the roofline object
+    # dominant kernel: the largest share of a step (time per launch x
+    # launches per step: the fused plan replays 100 times per step)
     dom = None
     for fname, fam in fams.items():
         for k, r in fam.get("ops", {}).items():
-            if dom is None or r["ms"] > dom[2]["ms"]:
+            if dom is None or r["ms"] * r.get("launches", 1) > dom[2]["ms"] * dom[2].get("launches", 1):
                 dom = (fname, k, r)
     roofline = None
     if dom is not None:
@@ -502,6 +508,8 @@ def main():
                         "achieved": round(r["TFLOP/s"], 1), "peak": r["peak"], "unit": "TFLOP/s",
                         "frac": round(r["frac"], 4), "traffic": PMC_TRAFFIC_BYTES.get(op)}
         roofline["traffic_unit"] = "bytes per launch (HBM, PMC)"
+        roofline["share_of_step"] = round(r["ms"] * r.get("launches", 1) / sum(
+            f["ms_per_step"] for f in fams.values()), 4)
     # every timed kernel against its own roofline
     kernels = []
     for fname, fam in fams.items():
@@ -533,10 +541,17 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (SplitMix64/Box-Muller, fixed seeds)",
-        "config": {"workload": fams.get("reduce", {}).get("workload", ""),
+        "config": {"workload": "; ".join(fams[f]["workload"] for f in ("reduce", "fused", "gemm") if f in fams),
                    "families": sorted(fams)},
         "families": {k: {kk: vv for kk, vv in v.items()} for k, v in fams.items()},
         "roofline": roofline,
+        # the north-star kernel (bf16 batched GEMM) against the dense bf16 MFMA peak
+        "gemm_bf16_roofline": ({"kernel": fams["gemm"]["ops"]["bf16"]["kernel"],
+                                "achieved": round(fams["gemm"]["ops"]["bf16"]["TFLOP/s"], 1),
+                                "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
+                                "frac": round(fams["gemm"]["ops"]["bf16"]["frac"], 4),
+                                "traffic": PMC_TRAFFIC_BYTES.get("gemm:bf16")}
+                               if "gemm" in fams and "bf16" in fams["gemm"]["ops"] else None),
         "kernels": kernels,
         "config5_mlp": extra.get("mlp"),
         "config3_eager": extra.get("eager"),

@@ -333,6 +333,44 @@ pt_status pt_where(const void *cond, int dtype_cond, const size_t *strides_cond,
 /* Replaces the fill kernels of factory_kernels.cu (zeros/ones/full). */
 pt_status pt_fill(void *out, int dtype, size_t n, const pt_scalar_t *value, pt_stream_t stream);
 
+/* --------------------------------------------------------------- indexed --
+ * Replaces cuda_validate_indices, cuda_launch_gather, cuda_launch_scatter_add
+ * (src/backends/cuda/indexed_ops.h:25-42), called from cuda_tensor_gather /
+ * cuda_tensor_scatter_add (src/cuda_array/ca_private.c:916-1007) and from
+ * Fusion's indexed native steps (src/fusion_execute.c:198-226).
+ *
+ * Indices are int32 with the input's rank; outside the indexed axis the
+ * index shape equals the input shape.  A validation record is a device
+ * int32[3] {operation, index, axis_size}: operation 0 = valid, 1 = a gather
+ * index, 2 = a scatter-add index outside [0, axis_size) (the first one a
+ * kernel meets; cuda_index_validation_result, indexed_ops.h:11-23).
+ *
+ * pt_index_validate clears `record` and checks every index against
+ * [0, axis_size), writing operation 1 on the first invalid one; the caller
+ * downloads the record (12 bytes) to learn the outcome, as ca_private.c:924
+ * does before it launches. */
+pt_status pt_index_validate(const int32_t *indices, const int *index_shape, const size_t *index_strides,
+                            size_t index_offset, int ndims, int axis, int axis_size, int32_t *record,
+                            pt_stream_t stream);
+/* out[c] = input[c with c[axis] := indices[c]] for every coordinate c of the
+ * index shape; out is contiguous row-major of the index shape and the
+ * input's dtype (any dtype: elements are copied bit for bit).  With
+ * validation != NULL an invalid index writes 0 to its output and is recorded
+ * there (the caller clears the record first, e.g. with pt_memset); with NULL
+ * the caller has validated the indices. */
+pt_status pt_gather(const void *input, int dtype, const int *input_shape, const size_t *input_strides,
+                    size_t input_offset, const int32_t *indices, const int *index_shape,
+                    const size_t *index_strides, size_t index_offset, int ndims, int axis, void *output,
+                    int32_t *validation, pt_stream_t stream);
+/* output[c with c[axis] := indices[c]] += updates[c] (atomic float32 /
+ * float64 adds; the order of adds to one element is not fixed).  The
+ * caller first copies the input into `output` (strides output_strides,
+ * extent axis_size along the axis), as cuda_launch_scatter_copy does. */
+pt_status pt_scatter_add(const int32_t *indices, const int *index_shape, const size_t *index_strides,
+                         size_t index_offset, const void *updates, const size_t *update_strides,
+                         size_t update_offset, int dtype, int ndims, int axis, int axis_size, void *output,
+                         const size_t *output_strides, int32_t *validation, pt_stream_t stream);
+
 /* ------------------------------------------------------ runtime compile --
  * Replaces cuda_compile_generated_source (src/compiler_ce.h:15) + NVRTC
  * (compiler_ce.c:513-560) + cuModuleLoadData/cuModuleGetFunction

@@ -754,3 +754,80 @@ int or_where(const void *cond, int dtype_c, const int *shape_c, int nd_c,
     }
     return OR_OK;
 }
+
+/* Offsets of index-shape coordinate `flat` in x (with the axis coordinate
+ * left out) and the coordinate itself (indexed_ops.cu:113-124). */
+static size_t indexed_offset(const int *shape_idx, const size_t *sx, int ndims, int axis, size_t flat)
+{
+    size_t off = 0;
+    for (int d = ndims - 1; d >= 0; d--) {
+        size_t c = flat % (size_t)shape_idx[d];
+        flat /= (size_t)shape_idx[d];
+        if (d != axis)
+            off += c * sx[d];
+    }
+    return off;
+}
+
+static int indexed_check(const int *shape_x, const int32_t *idx, const int *shape_idx, int ndims, int axis,
+                         int32_t *bad)
+{
+    if (ndims < 1 || ndims > OR_MAX_DIMS || axis < 0 || axis >= ndims)
+        return OR_EINVAL;
+    for (int d = 0; d < ndims; d++)
+        if (d != axis && shape_x[d] != shape_idx[d])
+            return OR_EINVAL;
+    size_t n = shape_elements(shape_idx, ndims);
+    for (size_t i = 0; i < n; i++)
+        if (idx[i] < 0 || idx[i] >= shape_x[axis]) {
+            if (bad)
+                *bad = idx[i];
+            return OR_EINVAL;
+        }
+    return OR_OK;
+}
+
+/* gather_kernel (indexed_ops.cu:108-133) over contiguous operands. */
+int or_gather(const void *x, int dtype, const int *shape_x, const int32_t *idx,
+              const int *shape_idx, int ndims, int axis, void *out, int32_t *bad)
+{
+    if (!valid_dtype(dtype))
+        return OR_EINVAL;
+    int st = indexed_check(shape_x, idx, shape_idx, ndims, axis, bad);
+    if (st != OR_OK)
+        return st;
+    size_t sx[OR_MAX_DIMS];
+    contiguous_strides(shape_x, ndims, sx);
+    size_t es = dtype_bytes(dtype), n = shape_elements(shape_idx, ndims);
+    for (size_t i = 0; i < n; i++) {
+        size_t off = indexed_offset(shape_idx, sx, ndims, axis, i) + (size_t)idx[i] * sx[axis];
+        memcpy((char *)out + i * es, (const char *)x + off * es, es);
+    }
+    return OR_OK;
+}
+
+/* scatter_copy + scatter_add_kernel (indexed_ops.cu:135-151, 179-204):
+ * the adds are applied in flat index order. */
+int or_scatter_add(const void *x, int dtype, const int *shape_x, const int32_t *idx,
+                   const int *shape_idx, const void *upd, int ndims, int axis,
+                   void *out, int32_t *bad)
+{
+    if (dtype != OR_F32 && dtype != OR_F64)
+        return OR_EINVAL;
+    int st = indexed_check(shape_x, idx, shape_idx, ndims, axis, bad);
+    if (st != OR_OK)
+        return st;
+    size_t sx[OR_MAX_DIMS];
+    contiguous_strides(shape_x, ndims, sx);
+    size_t es = dtype_bytes(dtype);
+    memcpy(out, x, shape_elements(shape_x, ndims) * es);
+    size_t n = shape_elements(shape_idx, ndims);
+    for (size_t i = 0; i < n; i++) {
+        size_t off = indexed_offset(shape_idx, sx, ndims, axis, i) + (size_t)idx[i] * sx[axis];
+        if (dtype == OR_F32)
+            ((float *)out)[off] += ((const float *)upd)[i];
+        else
+            ((double *)out)[off] += ((const double *)upd)[i];
+    }
+    return OR_OK;
+}

@@ -152,6 +152,24 @@ int or_where(const void *cond, int dtype_c, const int *shape_c, int nd_c,
              const void *y, const int *shape_y, int nd_y, int dtype_xy,
              void *out, const int *shape_out, int nd_out);
 
+/* ---- CudaArray::gather / scatterAdd along one axis -----------------------
+ * Restates the reference's gather_kernel / scatter_add_kernel
+ * (src/backends/cuda/indexed_ops.cu:108-133, 179-204; the HostArray has no
+ * indexed ops) for contiguous operands: for every coordinate c of the index
+ * shape, gather writes out[c] = x[c with c[axis] := idx[c]] (elements copied
+ * bitwise); scatter-add starts from a copy of x and adds upd[c] at that
+ * position, in flat index order (f32 / f64 only).  Returns OR_EINVAL with
+ * *bad = the first index outside [0, shape_x[axis]) (cuda_validate_indices,
+ * indexed_ops.cu:226-256).
+ * Pinned by: numpy take_along_axis (gather) and np.add.at (scatter-add) on
+ * random shapes and axes, and the reference's cudaarray_extended.phpt /
+ * indexed_low_precision.phpt vectors. */
+int or_gather(const void *x, int dtype, const int *shape_x, const int32_t *idx,
+              const int *shape_idx, int ndims, int axis, void *out, int32_t *bad);
+int or_scatter_add(const void *x, int dtype, const int *shape_x, const int32_t *idx,
+                   const int *shape_idx, const void *upd, int ndims, int axis,
+                   void *out, int32_t *bad);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,112 @@
+// Internal header of the GEMM kernels (pt_gemm.hip, pt_gemm_ring.hip):
+// argument block, element traits, MFMA fragment types and helpers shared by
+// the kernels.  Not part of the public boundary (include/pt_hip.h is).
+#pragma once
+
+#include "pt_common.h"
+
+namespace pt {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+#define GEMM_MAX_BATCH_DIMS 8
+
+struct GemmArgs {
+    const void *a;
+    const void *b;
+    void *c;
+    int M, N, K;
+    long long a_sm, a_sk;  // A(m,k) = a[m * a_sm + k * a_sk]
+    long long b_sk, b_sn;  // B(k,n) = b[k * b_sk + n * b_sn]
+    int tiles_m, tiles_n;
+    int batch;
+    int nbd;               // batch dims
+    int bshape[GEMM_MAX_BATCH_DIMS];
+    long long bsa[GEMM_MAX_BATCH_DIMS];
+    long long bsb[GEMM_MAX_BATCH_DIMS];
+    int remap;             // total tiles divisible by 8: XCD remap on
+    int vec_a, vec_b;      // 16-byte aligned packs: the checked kernel loads in-range packs whole
+    int ksplit, k_chunk;   // split-K: blockIdx.y = K chunk of k_chunk (a multiple of BK)
+    float *partial;        // split-K fp32 partials [ksplit][batch][M][N]
+};
+
+// Element traits: storage type and elements per 16-byte pack.
+template <int DT> struct GE;
+template <> struct GE<PT_BFLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
+template <> struct GE<PT_FLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
+template <> struct GE<PT_FLOAT32> { using S = float; static constexpr int PK = 4; };
+
+template <int DT>
+__device__ __forceinline__ void store_c(void *c, size_t idx, float v)
+{
+    if constexpr (DT == PT_FLOAT32) ((float *)c)[idx] = v;
+    else if constexpr (DT == PT_BFLOAT16) ((uint16_t *)c)[idx] = float_to_bf16(v);
+    else ((uint16_t *)c)[idx] = float_to_f16(v);
+}
+
+template <int DT> struct FragT;
+template <> struct FragT<PT_BFLOAT16> { using type = bf16x8_t; };
+template <> struct FragT<PT_FLOAT16> { using type = f16x8_t; };
+template <> struct FragT<PT_FLOAT32> { using type = floatx4; };
+
+// acc[i][j] += A-fragment i x B-fragment j for one k-slice.
+template <int DT, int TM, int TN>
+__device__ __forceinline__ void mfma_block(floatx16 (&acc)[TM][TN],
+                                           const typename FragT<DT>::type (&fa)[TM],
+                                           const typename FragT<DT>::type (&fb)[TN])
+{
+    if constexpr (DT == PT_FLOAT32) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                if constexpr (DT == PT_BFLOAT16)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+            }
+    }
+}
+
+__device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long long &oa, long long &ob)
+{
+    oa = 0;
+    ob = 0;
+    for (int d = g.nbd - 1; d >= 0; d--) {
+        int c = b % g.bshape[d];
+        b /= g.bshape[d];
+        oa += (long long)c * g.bsa[d];
+        ob += (long long)c * g.bsb[d];
+    }
+}
+
+#define PT_LDS_AS __attribute__((address_space(3)))
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int swz_k(int row, int cpr)
+{
+    return cpr == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
+}
+
+// 4-wave LDS-ring kernel for 16-bit operands (pt_gemm_ring.hip).  A variant
+// is a (K step, stages, tile width, workgroups per CU) shape; every variant
+// needs M % 256 == 0, N % tile width == 0 and K a multiple of gemm_ring_kmul.
+// b_row: B is n-contiguous (else k-contiguous).
+int gemm_ring_variants();
+int gemm_ring_bn(int variant);
+int gemm_ring_bk(int variant);
+int gemm_ring_kmul(int variant);
+void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s);
+
+}  // namespace pt

@@ -32,47 +32,9 @@
 #include <mutex>
 #include <string>
 
+#include "pt_gemm.h"
+
 namespace pt {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-#define GEMM_MAX_BATCH_DIMS 8
-
-struct GemmArgs {
-    const void *a;
-    const void *b;
-    void *c;
-    int M, N, K;
-    long long a_sm, a_sk;  // A(m,k) = a[m * a_sm + k * a_sk]
-    long long b_sk, b_sn;  // B(k,n) = b[k * b_sk + n * b_sn]
-    int tiles_m, tiles_n;
-    int batch;
-    int nbd;               // batch dims
-    int bshape[GEMM_MAX_BATCH_DIMS];
-    long long bsa[GEMM_MAX_BATCH_DIMS];
-    long long bsb[GEMM_MAX_BATCH_DIMS];
-    int remap;             // total tiles divisible by 8: XCD remap on
-    int vec_a, vec_b;      // 16-byte aligned packs: the checked kernel loads in-range packs whole
-    int ksplit, k_chunk;   // split-K: blockIdx.y = K chunk of k_chunk (a multiple of BK)
-    float *partial;        // split-K fp32 partials [ksplit][batch][M][N]
-};
-
-// Element traits: storage type and elements per 16-byte pack.
-template <int DT> struct GE;
-template <> struct GE<PT_BFLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
-template <> struct GE<PT_FLOAT16> { using S = uint16_t; static constexpr int PK = 8; };
-template <> struct GE<PT_FLOAT32> { using S = float; static constexpr int PK = 4; };
-
-template <int DT>
-__device__ __forceinline__ void store_c(void *c, size_t idx, float v)
-{
-    if constexpr (DT == PT_FLOAT32) ((float *)c)[idx] = v;
-    else if constexpr (DT == PT_BFLOAT16) ((uint16_t *)c)[idx] = float_to_bf16(v);
-    else ((uint16_t *)c)[idx] = float_to_f16(v);
-}
 
 // 16-byte pack type for register staging.
 typedef uint32_t Pack __attribute__((ext_vector_type(4)));
@@ -264,50 +226,6 @@ struct TileLoader {
         }
     }
 };
-
-template <int DT> struct FragT;
-template <> struct FragT<PT_BFLOAT16> { using type = bf16x8_t; };
-template <> struct FragT<PT_FLOAT16> { using type = f16x8_t; };
-template <> struct FragT<PT_FLOAT32> { using type = floatx4; };
-
-// acc[i][j] += A-fragment i x B-fragment j for one k-slice.
-template <int DT, int TM, int TN>
-__device__ __forceinline__ void mfma_block(floatx16 (&acc)[TM][TN],
-                                           const typename FragT<DT>::type (&fa)[TM],
-                                           const typename FragT<DT>::type (&fb)[TN])
-{
-    if constexpr (DT == PT_FLOAT32) {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][e], fb[j][e], acc[i][j], 0, 0, 0);
-    } else {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                if constexpr (DT == PT_BFLOAT16)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-                else
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-            }
-    }
-}
-
-__device__ __forceinline__ void batch_offsets(const GemmArgs &g, int b, long long &oa, long long &ob)
-{
-    oa = 0;
-    ob = 0;
-    for (int d = g.nbd - 1; d >= 0; d--) {
-        int c = b % g.bshape[d];
-        b /= g.bshape[d];
-        oa += (long long)c * g.bsa[d];
-        ob += (long long)c * g.bsb[d];
-    }
-}
 
 // LDS layout of one stage.  fp32 operands whose r is contiguous in memory
 // stay k-major in LDS ([k][r], row pitch r + 8: the two half-waves of a
@@ -561,14 +479,6 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
 // tell the DMA writes into one stage from the fragment reads of the other.
 // 8 waves (2 x 4) with 128 x 64 wave tiles; BK = 64 in two stages: the
 // loads of step k+1 run while step k is on the matrix cores.
-#define PT_LDS_AS __attribute__((address_space(3)))
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int swz_k(int row, int cpr)
-{
-    return cpr == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
-}
-
 template <int DT, bool B_KC>
 __global__ __launch_bounds__(512, 1) void k_gemm_direct(GemmArgs g)
 {
@@ -778,13 +688,17 @@ enum GemmTile {
     TILE_256x128 = 0, TILE_128x128 = 1, TILE_64x64 = 2, TILE_256x256 = 3,
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
     TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_128x128_W8_K2 = 11,
-    TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13, TILE_COUNT = 14
+    TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13,
+    // 4-wave LDS-ring kernels (k_gemm_ring): BK x stages
+    TILE_RING_FIRST = 14, TILE_RING_LAST = 23,  // variants 0..9 of gemm_ring_variants()
+    TILE_COUNT = 24
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
     {256, 128, 1}, {128, 128, 1}, {64, 64, 1}, {256, 256, 1}, {256, 128, 2}, {256, 256, 2},
     {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}, {128, 128, 2},
-    {128, 64, 1}, {128, 64, 2}};
+    {128, 64, 1}, {128, 64, 2}, {256, 256, 1}, {256, 256, 2}, {256, 256, 1}, {256, 256, 1},
+    {256, 256, 1}, {256, 128, 1}, {256, 128, 1}, {256, 256, 2}, {256, 256, 1}, {256, 128, 1}};
 
 static int g_tile_override = -1;
 
@@ -993,6 +907,31 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     if (dtype != PT_FLOAT32 && (tile == TILE_128x128_W8_K2 || tile == TILE_128x64_W4M2 || tile == TILE_128x64_W4M2_K2))
         tile = TILE_128x128;
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
+    if (tile >= TILE_RING_FIRST && tile <= TILE_RING_LAST) {
+        // 4-wave LDS-ring kernel: 16-bit operands, whole tiles (256 rows,
+        // 256 or 128 columns), K a multiple of gemm_ring_kmul, k-contiguous A,
+        // B k- or n-contiguous, 16-byte aligned rows and batch offsets
+        const int variant = tile - TILE_RING_FIRST;
+        const int kmul = gemm_ring_kmul(variant), bn = gemm_ring_bn(variant);
+        const bool b_row = g.b_sn == 1, b_col = g.b_sk == 1;
+        const long long ldb = b_row ? g.b_sk : g.b_sn;
+        bool ok = dtype != PT_FLOAT32 && g.a_sk == 1 && (b_row || b_col) && g.M % 256 == 0 && g.N % bn == 0 &&
+                  g.K % kmul == 0 && aligned(a) && aligned(b) && g.a_sm % 8 == 0 && ldb % 8 == 0;
+        for (int d = 0; d < g.nbd; d++)
+            if (g.bsa[d] % 8 || g.bsb[d] % 8) ok = false;
+        long long tiles = (long long)(g.M / 256) * (g.N / bn) * batch;
+        if (ok && tiles <= 0x7fffffffLL) {
+            g.tiles_m = g.M / 256;
+            g.tiles_n = g.N / bn;
+            g.remap = tiles % 8 == 0;
+            launch_gemm_ring(g, dtype, b_row, variant, dim3((unsigned)tiles), s);
+            PT_LAUNCH_CHECK("matmul");
+            counters().mfma_gemm_calls++;
+            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "mfma-lds-ring%s", suffix);
+            return PT_OK;
+        }
+        tile = TILE_256x256_DIRECT;
+    }
     if (tile == TILE_256x256_DIRECT) {
         // direct-to-LDS kernel: 16-bit operands, whole 256x256 tiles, K a
         // multiple of 64, k-contiguous A, B k- or n-contiguous, 16-byte

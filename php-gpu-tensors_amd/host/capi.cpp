@@ -4,6 +4,8 @@
 #include "phpt_host.h"
 #include "runtime.hpp"
 
+#include <limits.h>
+
 #include <string.h>
 
 using namespace phpt;
@@ -269,6 +271,40 @@ phpt_tensor *phpt_where(phpt_tensor *c, phpt_tensor *x, phpt_tensor *y)
 {
     clear_error();
     return wrap(cuda_tensor_where(c->t, x->t, y->t));
+}
+
+// cuda_array_index_axis (cuda_array_ce.c:2405-2421): negative axes count
+// from the end
+static bool index_axis(const TensorP &t, long long requested, int *axis)
+{
+    if (requested < INT_MIN || requested > INT_MAX) {
+        set_invalid("Indexed operation axis is outside the supported integer range");
+        return false;
+    }
+    int normalized = (int)requested;
+    if (normalized < 0) normalized += t->ndims;
+    if (normalized < 0 || normalized >= t->ndims) {
+        set_invalid("Indexed operation axis is out of range for tensor rank %d", t->ndims);
+        return false;
+    }
+    *axis = normalized;
+    return true;
+}
+
+phpt_tensor *phpt_gather(phpt_tensor *a, phpt_tensor *indices, long long axis)
+{
+    clear_error();
+    int ax;
+    if (!index_axis(a->t, axis, &ax)) return nullptr;
+    return wrap(cuda_tensor_gather(a->t, indices->t, ax));
+}
+
+phpt_tensor *phpt_scatter_add(phpt_tensor *a, phpt_tensor *indices, phpt_tensor *updates, long long axis)
+{
+    clear_error();
+    int ax;
+    if (!index_axis(a->t, axis, &ax)) return nullptr;
+    return wrap(cuda_tensor_scatter_add(a->t, indices->t, updates->t, ax));
 }
 
 phpt_tensor *phpt_astype(phpt_tensor *a, int dtype)

@@ -174,6 +174,12 @@ struct Plan {
     bool workspace_sized = false;
     size_t workspace_bytes = 0;
     std::shared_ptr<Storage> workspace;
+    // indexed native steps (gather / scatterAdd): their invalid indices are
+    // recorded in a device record that every execution clears and reads
+    // back once (fusion_execute.c:630-645, 755-775); such plans neither
+    // capture into a graph nor run asynchronously
+    bool indexed = false;
+    std::shared_ptr<Storage> index_record;
 };
 
 static bool is_elementwise(const FusionNode &n)
@@ -1235,9 +1241,17 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         emit_general(*p, k, os);
     }
     p->source = os.str();
-    // graph compatibility: every step can be captured except native steps
-    // whose kernels need host-side choices per call (none here) -- plans
-    // with views of intermediates still replay eagerly between kernels
+    // graph compatibility: every step can be captured except indexed native
+    // steps, whose validation is read back on the host after each execution
+    for (const Step &st : p->steps) {
+        if (!st.native) continue;
+        const int kind = p->items[st.item].t->node->native.kind;
+        if (kind == NAT_GATHER || kind == NAT_SCATTER_ADD) p->indexed = true;
+    }
+    if (p->indexed) {
+        p->graph_compatible = false;
+        p->incompatibility = "indexed native steps validate their indices on the host";
+    }
     return p;
 }
 
@@ -1538,6 +1552,46 @@ static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, boo
     return true;
 }
 
+static bool collect_outputs(Plan &p, std::vector<TensorP> &vals, std::vector<TensorP> &outs, uint64_t t0,
+                            uint64_t t1);
+
+// A plan with indexed native steps: clear the plan's validation record, run
+// the steps with the indexed natives recording into it, then read it back
+// (the execution's one synchronization) and raise the first invalid index
+// as the reference does (fusion_execute.c:755-775).
+static bool execute_indexed(Plan &p, std::vector<TensorP> &vals, std::vector<TensorP> &outs, uint64_t t0,
+                            uint64_t t1)
+{
+    if (!p.index_record) {
+        auto st = std::make_shared<Storage>();
+        if (!check_status(pt_alloc(&st->ptr, 3 * sizeof(int32_t), nullptr), "Fusion index validation buffer"))
+            return false;
+        st->bytes = 3 * sizeof(int32_t);
+        p.index_record = st;
+    }
+    if (!check_status(pt_memset(p.index_record->ptr, 0, 3 * sizeof(int32_t), nullptr),
+                      "Fusion index validation reset"))
+        return false;
+    index_record() = (int32_t *)p.index_record->ptr;
+    bool ok = run_steps(p, vals);
+    index_record() = nullptr;
+    if (!ok) return false;
+    int32_t rec[3] = {0, 0, 0};
+    if (!check_status(pt_memcpy_d2h(rec, p.index_record->ptr, sizeof(rec), nullptr),
+                      "Fusion index validation synchronization failed"))
+        return false;
+    p.synchronizations++;
+    if (rec[0] == 1) {
+        set_invalid("gather indices must be within [0, %d)", rec[2]);
+        return false;
+    }
+    if (rec[0] == 2) {
+        set_invalid("scatterAdd indices must be within [0, %d)", rec[2]);
+        return false;
+    }
+    return collect_outputs(p, vals, outs, t0, t1);
+}
+
 static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<TensorP> &outs, bool wait)
 {
     uint64_t t0 = now_ns();
@@ -1584,12 +1638,19 @@ static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<Ten
             p.graph_launches++;
         }
     } else if (!ran) {
+        if (p.indexed) return execute_indexed(p, vals, outs, t0, t1);
         if (!run_steps(p, vals)) return false;
     }
     if (wait) {
         if (!check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed")) return false;
         p.synchronizations++;
     }
+    return collect_outputs(p, vals, outs, t0, t1);
+}
+
+static bool collect_outputs(Plan &p, std::vector<TensorP> &vals, std::vector<TensorP> &outs, uint64_t t0,
+                            uint64_t t1)
+{
     uint64_t t2 = now_ns();
     outs.clear();
     for (int id : p.outputs) {
@@ -1863,6 +1924,10 @@ phpt_execution *phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ni
 {
     clear_error();
     Plan &p = *g->plan;
+    if (p.indexed) {
+        set_runtime("FusionGraph::runAsync is not available for plans with indexed operations");
+        return nullptr;
+    }
     std::vector<TensorP> ins, outs;
     if (!bind(p, inputs, ninputs, ins)) return nullptr;
     if (!execute(p, ins, outs, false)) return nullptr;
@@ -1942,7 +2007,7 @@ const char *phpt_graph_stats(phpt_graph *g)
        << ";viewAliases=" << aliases << ";executions=" << p.executions << ";executionSteps=" << p.steps.size() + aliases
        << ";intermediateBuffers=" << intermediates << ";cacheHit=" << (p.cache_hit ? 1 : 0)
        << ";backend=" << (p.use_graph ? "cuda-graph" : "stream")
-       << ";asyncCompatible=1;cudaGraphCompatible=" << (p.graph_compatible ? 1 : 0)
+       << ";asyncCompatible=" << (p.indexed ? 0 : 1) << ";cudaGraphCompatible=" << (p.graph_compatible ? 1 : 0)
        << ";graphReplay=" << (p.use_graph && !native_present ? 1 : 0)
        << ";graphLaunches=" << p.graph_launches << ";bufferReuses=" << p.buffer_reuses
        << ";pending=" << p.pending << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)
@@ -1966,7 +2031,8 @@ const char *phpt_graph_plan(phpt_graph *g)
     for (Step &st : p.steps) {
         if (st.native) {
             static const char *names[] = {"native-matmul", "native-reduction", "native-reduction",
-                                          "native-moments", "native-softmax", "native-layernorm"};
+                                          "native-moments", "native-softmax", "native-layernorm",
+                                          "native-gather", "native-scatter-add"};
             const Item &it = p.items[st.item];
             // layout aliases: views passed to this native step without a copy
             for (int a : it.args)

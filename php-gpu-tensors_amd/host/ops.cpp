@@ -195,6 +195,124 @@ TensorP cuda_tensor_where(const TensorP &c, const TensorP &x, const TensorP &y)
     return out;
 }
 
+// ------------------------------------------------------------- indexed ops
+// Device validation record of the Fusion plan being executed: while set,
+// indexed natives record invalid indices there (one download per plan
+// execution) instead of validating before they launch.
+int32_t *&index_record()
+{
+    static thread_local int32_t *record = nullptr;
+    return record;
+}
+
+// cuda_tensor_validate_indexed_shapes (ca_private.c:885-914)
+static bool validate_indexed_shapes(const TensorP &input, const TensorP &indices, const TensorP &updates, int axis,
+                                    const char *operation)
+{
+    if (!input || !indices || axis < 0 || axis >= input->ndims || indices->ndims != input->ndims ||
+        indices->dtype != PT_INT32) {
+        set_invalid("%s requires int32 indices with the same rank and a valid axis", operation);
+        return false;
+    }
+    for (int d = 0; d < input->ndims; d++) {
+        if (d != axis && input->shape[d] != indices->shape[d]) {
+            set_invalid("%s input and index shapes must match outside the indexed axis", operation);
+            return false;
+        }
+        if (updates && updates->shape[d] != indices->shape[d]) {
+            set_invalid("%s updates must have the same shape as indices", operation);
+            return false;
+        }
+    }
+    if (updates && updates->dtype != input->dtype) {
+        set_invalid("%s input and updates must have the same dtype", operation);
+        return false;
+    }
+    return true;
+}
+
+// Eager validation (cuda_validate_indices before the launch): one device
+// pass, then a 12-byte download of the record.
+static bool validate_indices(const TensorP &indices, int axis, int axis_size, const char *operation)
+{
+    if (!indices->numel()) return true;
+    void *rec = nullptr;
+    if (!check_status(pt_alloc(&rec, 3 * sizeof(int32_t), nullptr), "Failed to validate indices")) return false;
+    int32_t host[3] = {0, 0, 0};
+    bool ok = check_status(pt_index_validate((const int32_t *)base_ptr(indices), indices->shape, indices->strides,
+                                             indices->offset, indices->ndims, axis, axis_size, (int32_t *)rec,
+                                             nullptr),
+                           "Failed to validate indices") &&
+              check_status(pt_memcpy_d2h(host, rec, sizeof(host), nullptr), "Failed to validate indices");
+    pt_free(rec, nullptr);
+    if (ok && host[0] != 0) {
+        set_invalid("%s indices must be within [0, %d)", operation, axis_size);
+        return false;
+    }
+    return ok;
+}
+
+TensorP cuda_tensor_gather(const TensorP &input, const TensorP &indices, int axis)
+{
+    if (!validate_indexed_shapes(input, indices, nullptr, axis, "gather")) return nullptr;
+    if (fusion_active()) {
+        NativeSpec sp;
+        sp.kind = NAT_GATHER;
+        sp.axis = axis;
+        return fusion_record_native(sp, {input, indices}, indices->shape, indices->ndims, input->dtype);
+    }
+    if (!guard(input) || !guard(indices)) return nullptr;
+    int32_t *record = index_record();
+    if (!record && !validate_indices(indices, axis, input->shape[axis], "gather")) return nullptr;
+    TensorP out = output_tensor(indices->shape, indices->ndims, input->dtype);
+    if (!out || !out->numel()) return out;
+    if (!check_status(pt_gather(base_ptr(input), input->dtype, input->shape, input->strides, input->offset,
+                                (const int32_t *)base_ptr(indices), indices->shape, indices->strides,
+                                indices->offset, input->ndims, axis, out->storage->ptr, record, nullptr),
+                      "gather kernel failed"))
+        return nullptr;
+    return out;
+}
+
+TensorP cuda_tensor_scatter_add(const TensorP &input, const TensorP &indices, const TensorP &updates, int axis)
+{
+    if (!validate_indexed_shapes(input, indices, updates, axis, "scatterAdd")) return nullptr;
+    // float16 / bfloat16 run in float32 (ca_private.c:957-968): the result is float32
+    const bool low = input->dtype == PT_FLOAT16 || input->dtype == PT_BFLOAT16;
+    const int dt = low ? PT_FLOAT32 : input->dtype;
+    if (dt != PT_FLOAT32 && dt != PT_FLOAT64) {
+        set_invalid("scatterAdd currently supports float32 and float64 tensors");
+        return nullptr;
+    }
+    if (fusion_active()) {
+        NativeSpec sp;
+        sp.kind = NAT_SCATTER_ADD;
+        sp.axis = axis;
+        return fusion_record_native(sp, {input, indices, updates}, input->shape, input->ndims, dt);
+    }
+    if (!guard(input) || !guard(indices) || !guard(updates)) return nullptr;
+    TensorP in = input, up = updates;
+    if (low) {
+        in = tensor_cast(input, PT_FLOAT32);
+        up = in ? tensor_cast(updates, PT_FLOAT32) : nullptr;
+        if (!up) return nullptr;
+    }
+    int32_t *record = index_record();
+    if (!record && !validate_indices(indices, axis, input->shape[axis], "scatterAdd")) return nullptr;
+    TensorP out = output_tensor(in->shape, in->ndims, dt);
+    if (!out || !out->numel()) return out;
+    // the input's values first (cuda_launch_scatter_copy), then the adds
+    if (!check_status(pt_cast(base_ptr(in), dt, in->strides, in->offset, out->storage->ptr, dt, in->shape, in->ndims,
+                              nullptr),
+                      "scatterAdd kernel failed") ||
+        !check_status(pt_scatter_add((const int32_t *)base_ptr(indices), indices->shape, indices->strides,
+                                     indices->offset, base_ptr(up), up->strides, up->offset, dt, in->ndims, axis,
+                                     in->shape[axis], out->storage->ptr, out->strides, record, nullptr),
+                      "scatterAdd kernel failed"))
+        return nullptr;
+    return out;
+}
+
 // ------------------------------------------------------------- reductions
 // calculate_reduction_shape (src/operations.c:37-67)
 static int reduction_shape(const Tensor &t, int axis, int *shape)
@@ -560,6 +678,8 @@ TensorP native_execute(const NativeSpec &sp, const std::vector<TensorP> &in)
     case NAT_ARG_REDUCE: return cuda_tensor_reduce_arg(in[0], sp.axis, sp.op);
     case NAT_MOMENTS: return cuda_array_variance(in[0], sp.axis, sp.correction, sp.std_dev);
     case NAT_SOFTMAX: return cuda_array_softmax(in[0], sp.axis);
+    case NAT_GATHER: return cuda_tensor_gather(in[0], in[1], sp.axis);
+    case NAT_SCATTER_ADD: return cuda_tensor_scatter_add(in[0], in[1], in[2], sp.axis);
     case NAT_LAYERNORM: {
         size_t k = 1;
         TensorP scale = sp.has_scale ? in[k++] : nullptr;

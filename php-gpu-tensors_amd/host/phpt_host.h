@@ -72,6 +72,10 @@ phpt_tensor *phpt_matmul(phpt_tensor *a, phpt_tensor *b);
 phpt_tensor *phpt_tune_matmul(phpt_tensor *a, phpt_tensor *b, int *tiles, float *median_ms,
                               int max_candidates, int *count, int *selected);
 phpt_tensor *phpt_where(phpt_tensor *c, phpt_tensor *x, phpt_tensor *y);
+/* CudaArray::gather / scatterAdd (cuda_array_ce.c:2423-2465): int32 indices,
+ * axis may be negative */
+phpt_tensor *phpt_gather(phpt_tensor *a, phpt_tensor *indices, long long axis);
+phpt_tensor *phpt_scatter_add(phpt_tensor *a, phpt_tensor *indices, phpt_tensor *updates, long long axis);
 phpt_tensor *phpt_astype(phpt_tensor *a, int dtype);
 phpt_tensor *phpt_copy(phpt_tensor *a);
 

@@ -139,6 +139,11 @@ TensorP cuda_tensor_matmul(const TensorP &a, const TensorP &b);
 TensorP cuda_tune_matmul(const TensorP &a, const TensorP &b, int *tiles, float *median_ms, int max_candidates,
                          int *count, int *selected);
 TensorP cuda_tensor_where(const TensorP &c, const TensorP &x, const TensorP &y);
+// gather / scatterAdd along `axis` (ca_private.c:916-1007); int32 indices
+TensorP cuda_tensor_gather(const TensorP &input, const TensorP &indices, int axis);
+TensorP cuda_tensor_scatter_add(const TensorP &input, const TensorP &indices, const TensorP &updates, int axis);
+// validation record of the executing Fusion plan (nullptr outside one)
+int32_t *&index_record();
 TensorP tensor_cast(const TensorP &a, int dtype);
 TensorP astype(const TensorP &a, int dtype);  // safe casts only (CudaArray::astype)
 TensorP copy(const TensorP &a);
@@ -159,7 +164,7 @@ enum NodeKind {
 };
 
 enum NativeKind {
-    NAT_MATMUL = 0, NAT_REDUCE, NAT_ARG_REDUCE, NAT_MOMENTS, NAT_SOFTMAX, NAT_LAYERNORM
+    NAT_MATMUL = 0, NAT_REDUCE, NAT_ARG_REDUCE, NAT_MOMENTS, NAT_SOFTMAX, NAT_LAYERNORM, NAT_GATHER, NAT_SCATTER_ADD
 };
 
 struct NativeSpec {

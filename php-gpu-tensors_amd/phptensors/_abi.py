@@ -133,6 +133,13 @@ SIGNATURES = {
                                c_int_p, ctypes.c_int, vp]),
     "pt_where": (ctypes.c_int, [vp, ctypes.c_int, c_size_p, vp, c_size_p, vp, c_size_p,
                                 ctypes.c_int, vp, c_int_p, ctypes.c_int, vp]),
+    "pt_index_validate": (ctypes.c_int, [vp, c_int_p, c_size_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_int, vp, vp]),
+    "pt_gather": (ctypes.c_int, [vp, ctypes.c_int, c_int_p, c_size_p, ctypes.c_size_t, vp, c_int_p, c_size_p,
+                                 ctypes.c_size_t, ctypes.c_int, ctypes.c_int, vp, vp, vp]),
+    "pt_scatter_add": (ctypes.c_int, [vp, c_int_p, c_size_p, ctypes.c_size_t, vp, c_size_p, ctypes.c_size_t,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, c_size_p, vp,
+                                      vp]),
     "pt_fill": (ctypes.c_int, [vp, ctypes.c_int, ctypes.c_size_t, ctypes.POINTER(PtScalar), vp]),
     "pt_rtc_compile": (ctypes.c_int, [ctypes.c_char_p, ctypes.c_char_p, ctypes.POINTER(vp),
                                       ctypes.c_char_p, ctypes.c_size_t]),

@@ -48,6 +48,8 @@ SIGNATURES = {
     "phpt_tune_matmul": (T, [T, T, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float), ctypes.c_int,
                              ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int)]),
     "phpt_where": (T, [T, T, T]),
+    "phpt_gather": (T, [T, T, ctypes.c_longlong]),
+    "phpt_scatter_add": (T, [T, T, T, ctypes.c_longlong]),
     "phpt_astype": (T, [T, ctypes.c_int]),
     "phpt_copy": (T, [T]),
     "phpt_fusion_begin": (ctypes.c_int, [ctypes.c_int]),

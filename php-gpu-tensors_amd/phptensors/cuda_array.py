@@ -557,6 +557,42 @@ class CudaArray:
             AG.record(out, [a, b], back, "matmul")
         return out
 
+    # ------------------------------------------------------------ indexed
+    def gather(self, indices, axis=0):
+        """out[c] = self[c with c[axis] := indices[c]] (int32 indices of the
+        same rank, cuda_array_ce.c:2423-2442); the gradient scatters the
+        upstream gradient back (autograd.c:1631-1646), in float32 for
+        float16 / bfloat16 inputs."""
+        if not isinstance(indices, CudaArray):
+            raise InvalidArgumentException("gather() expects CudaArray indices")
+        out = CudaArray._wrap(_host.load().phpt_gather(self._h, indices._h, int(axis)), "gather")
+        if AG.active(self):
+            src = self
+            ax = int(axis) % self.getNdims()
+
+            def back(g):
+                zdt = "float32" if src.getDtype() in ("float16", "bfloat16") else src.getDtype()
+                return [CudaArray.zeros(src.getShape(), zdt).scatterAdd(indices, g, ax)]
+            AG.record(out, [self], back, "gather")
+        return out
+
+    def scatterAdd(self, indices, updates, axis=0):
+        """A copy of self with updates[c] added at c with c[axis] :=
+        indices[c] (cuda_array_ce.c:2444-2465); float16 / bfloat16 run and
+        return float32.  Gradients: the input's is the upstream gradient,
+        the updates' its gather (autograd.c:1648-1652)."""
+        if not isinstance(indices, CudaArray) or not isinstance(updates, CudaArray):
+            raise InvalidArgumentException("scatterAdd() expects CudaArray indices and updates")
+        out = CudaArray._wrap(_host.load().phpt_scatter_add(self._h, indices._h, updates._h, int(axis)),
+                              "scatterAdd")
+        if AG.active(self, updates):
+            ax = int(axis) % self.getNdims()
+
+            def back(g):
+                return [g, g.gather(indices, ax) if AG.needs_grad(updates) else None]
+            AG.record(out, [self, updates], back, "scatterAdd")
+        return out
+
     # ------------------------------------------------------------ views
     def reshape(self, shape):
         sh, n = _ints(shape)

@@ -279,3 +279,43 @@ def where(cond, dtype_c, x, y, dtype_xy):
                           _p(x), _ints(x.shape), x.ndim, _p(y), _ints(y.shape), y.ndim,
                           dtype_xy, _p(out), _ints(shape), len(shape)), "where")
     return out
+
+
+class OracleIndexError(ValueError):
+    """An index outside [0, axis size); `index` is the first one met."""
+
+    def __init__(self, index):
+        super().__init__(f"index {index} out of range")
+        self.index = index
+
+
+def gather(x, dtype, indices, axis):
+    """CudaArray::gather semantics (indexed_ops.cu:108-133) on contiguous
+    storage arrays; raises OracleIndexError for an out-of-range index."""
+    x = np.ascontiguousarray(x)
+    idx = np.ascontiguousarray(indices, dtype=np.int32)
+    out = np.zeros(idx.shape, x.dtype)
+    bad = ctypes.c_int32(0)
+    st = lib().or_gather(_p(x), dtype, _ints(x.shape), _p(idx), _ints(idx.shape), x.ndim, axis % x.ndim,
+                         _p(out), ctypes.byref(bad))
+    if st != 0:
+        if idx.ndim == x.ndim and all(a == b for d, (a, b) in enumerate(zip(x.shape, idx.shape))
+                                      if d != axis % x.ndim):
+            raise OracleIndexError(bad.value)
+        _check(st, "gather")
+    return out
+
+
+def scatter_add(x, dtype, indices, updates, axis):
+    """CudaArray::scatterAdd semantics (indexed_ops.cu:135-204): a copy of x
+    with updates added at the indexed positions, in flat index order."""
+    x = np.ascontiguousarray(x)
+    idx = np.ascontiguousarray(indices, dtype=np.int32)
+    upd = np.ascontiguousarray(updates, dtype=x.dtype)
+    out = np.zeros_like(x)
+    bad = ctypes.c_int32(0)
+    st = lib().or_scatter_add(_p(x), dtype, _ints(x.shape), _p(idx), _ints(idx.shape), _p(upd), x.ndim,
+                              axis % x.ndim, _p(out), ctypes.byref(bad))
+    if st != 0:
+        raise OracleIndexError(bad.value)
+    return out

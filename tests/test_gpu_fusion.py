@@ -130,6 +130,69 @@ def test_tanh_x_plus_y_z_vs_oracle():
     assert d.max() <= 4
 
 
+def test_config3_full_size_replay_vs_oracle():
+    """The plan bench.py times (config 3), at its full size and seeds: x, z
+    [16384, 8192] U(-2, 2) (seeds 3, 31), y [8192] (seed 32), compiled with
+    cudaGraph=True and replayed from its HIP graph, as FusionGraph::run
+    replays it (fusion_execute.c:385-598).  Every 64th row and the last row of
+    the output are checked against the oracle's per-op composition: y*z and
+    x+m rounded per op (exact), tanh within 4 ulp of libm.  The sampled rows
+    span the whole grid, so the kernel's index decode is checked up to its
+    last elements."""
+    from phptensors import synthetic
+    rows, n = 16384, 8192
+    xs = synthetic.uniform((rows, n), -2.0, 2.0, seed=3)
+    zs = synthetic.uniform((rows, n), -2.0, 2.0, seed=31)
+    ys = synthetic.uniform((n,), -2.0, 2.0, seed=32)
+    x, y, z = (CudaArray.fromNumpy(v) for v in (xs, ys, zs))
+    graph = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z], cudaGraph=True)
+    graph.replay(3, x, y, z)
+    out = graph.run(x, y, z)
+    assert [s["kind"] for s in graph.getPlan()] == ["fused"]
+    assert graph.getStats()["graphLaunches"] >= 2
+    sample = np.r_[0:rows:64, rows - 1]
+    got = out.toNumpy()[sample]
+    mul = O.binary(ys, O.F32, zs[sample], O.F32, "mul", O.F32)
+    add = O.binary(xs[sample], O.F32, mul, O.F32, "add", O.F32)
+    ref = O.unary(add, O.F32, "tanh")
+    d = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+    assert d.max() <= 4, (int(d.max()), np.unravel_index(int(d.argmax()), d.shape))
+
+
+def test_plan_natives_vs_oracle():
+    """A captured plan whose native steps (GEMM, axis sum, max, argMax,
+    softmax) are checked against the oracle rather than the eager kernels,
+    on every replay.  Integer-valued operands make the GEMM, the bias add
+    and the sums exact in fp32, so those compare bitwise; softmax within
+    1e-5 relative (fusion_execute.c:98-290 runs these natives in plans)."""
+    r = np.random.default_rng(12)
+    an = r.integers(-3, 4, (512, 384)).astype(np.float32)
+    wn = r.integers(-3, 4, (384, 256)).astype(np.float32)
+    bn = r.integers(-3, 4, (256,)).astype(np.float32)
+    a, w, b = (CudaArray.fromNumpy(v) for v in (an, wn, bn))
+
+    def fn(x, m, bias):
+        h = x.matmul(m) + bias
+        return [h, h.sum(1), h.max(1), h.argMax(1), (h * 0.01).softmax(-1)]
+
+    graph = Fusion.compile(fn, [a, w, b], cudaGraph=True)
+    h_ref = O.binary(O.matmul(an, wn, O.F32), O.F32, bn, O.F32, "add", O.F32)
+    sum_ref, _ = O.reduce(h_ref, O.F32, "sum", 1)
+    max_ref, _ = O.reduce(h_ref, O.F32, "max", 1)
+    arg_ref = O.arg_reduce(h_ref, O.F32, "argmax", 1)
+    soft_ref = O.softmax_lastaxis(O.binary_scalar(h_ref, O.F32, 0.01, "mul", O.F32))
+    for rep in range(3):
+        h, hs, hm, ha, sm = graph.run(a, w, b)
+        np.testing.assert_array_equal(h.toNumpy(), h_ref)
+        np.testing.assert_array_equal(hs.toNumpy(), sum_ref)
+        np.testing.assert_array_equal(hm.toNumpy(), max_ref)
+        np.testing.assert_array_equal(ha.toNumpy(), arg_ref)
+        np.testing.assert_allclose(sm.toNumpy(), soft_ref, rtol=1e-5, atol=1e-12)
+    kinds = [s["kind"] for s in graph.getPlan()]
+    assert kinds.count("native") >= 5
+    assert graph.getStats()["graphLaunches"] >= 2
+
+
 def test_strided_and_broadcast_leaves_bitwise():
     base = CudaArray.fromNumpy(rand((96, 130), 7))
     v = base.transpose()                  # [130, 96] strided leaf

@@ -244,6 +244,33 @@ def test_config5_full_size_step():
     check_step(layers, rows, 5, params, out, x, y)
 
 
+def test_config5_compiled_plan_full_size_vs_oracle():
+    """The step bench.py times (config 5): mlp.compile_training_plan at batch
+    4096, 784-1024-1024-10, replayed from its HIP graph (natives inside,
+    three branches), checked against the float64 oracle like the eager step
+    (examples/08_gpu_classifier.php:117-161), and bitwise against the eager
+    step on the same inputs."""
+    layers, rows = (784, 1024, 1024, 10), 4096
+    params, xt, yt, x, y = make(rows, layers, 5)
+    opt = Optimizer.adamW()
+    state = opt.initState(params)
+    rate = CudaArray.full([1], 1e-3)
+    inputs = mlp.training_inputs(xt, yt, rate, params, state)
+    graph = mlp.compile_training_plan(inputs, opt)
+    graph.replay(2, *inputs)
+    p1, s1, loss1 = mlp.unpack_step(graph.run(*inputs))
+    assert graph.getStats()["graphLaunches"] >= 2
+    out = {"loss": loss1, "parameters": p1, "state": s1}
+    check_step(layers, rows, 5, params, out, x, y)
+    eager = mlp.train_batch(xt, yt, params, opt, state, rate)
+    assert loss1.toBits().tobytes() == eager["loss"].toBits().tobytes()
+    for a, b in zip(p1, eager["parameters"]):
+        assert a.toBits().tobytes() == b.toBits().tobytes()
+    for key in ("firstMoment", "secondMoment"):
+        for a, b in zip(s1[key], eager["state"][key]):
+            assert a.toBits().tobytes() == b.toBits().tobytes()
+
+
 def test_training_plan_groups_adamw_updates_like_the_reference():
     """tests/classifier_training.phpt:41-49: the training plan of a
     784-512-256-10 model keeps one fused dependent-output group per
