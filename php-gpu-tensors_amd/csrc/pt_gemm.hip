@@ -691,7 +691,10 @@ enum GemmTile {
     TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13,
     // 4-wave LDS-ring kernels (k_gemm_ring): BK x stages
     TILE_RING_FIRST = 14, TILE_RING_LAST = 23,  // variants 0..9 of gemm_ring_variants()
-    TILE_COUNT = 24
+    TILE_COUNT = 24,
+    // large 16-bit products: BK 64, two stages, interleaved schedule (the
+    // fastest ring shape measured on config 4)
+    TILE_RING_DEFAULT = TILE_RING_FIRST + 7
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
@@ -899,7 +902,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         // faster of the two for each layout of the config-5 products)
         const int mid32 = g.b_sn == 1 ? TILE_128x128_W8 : TILE_128x64_W4M2;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
-                   ? (dtype == PT_FLOAT32 ? TILE_256x128_W8 : TILE_256x256_DIRECT)
+                   ? (dtype == PT_FLOAT32 ? TILE_256x128_W8 : TILE_RING_DEFAULT)
                    : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? mid32 : TILE_128x128)
                                                 : TILE_64x64;
     }
@@ -1067,7 +1070,8 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
                                 TILE_256x128_W8, TILE_128x128_W8, TILE_128x128_W8_K2, TILE_128x64_W4M2,
                                 TILE_128x64_W4M2_K2};
     static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
-                                TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8};
+                                TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8, TILE_RING_DEFAULT,
+                                TILE_RING_FIRST + 8};
     const int *cands = dtype == PT_FLOAT32 ? kFp32 : kHalf;
     const int ncand = dtype == PT_FLOAT32 ? (int)(sizeof(kFp32) / sizeof(int)) : (int)(sizeof(kHalf) / sizeof(int));
     hipStream_t s = stream_of(stream);

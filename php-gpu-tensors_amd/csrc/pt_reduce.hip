@@ -67,12 +67,15 @@ __device__ __forceinline__ void load_chunk(const typename RT<DT>::S *p, typename
     }
 }
 
-// 16-byte store of a register chunk.
+// 16-byte store of a register chunk; NT: nontemporal (streaming output
+// that is not read back by this kernel).
+template <bool NT = false>
 __device__ __forceinline__ void store16(void *dst, const void *src)
 {
     u32x4 v;
     memcpy(&v, src, 16);
-    *(u32x4 *)dst = v;
+    if constexpr (NT) __builtin_nontemporal_store(v, (u32x4 *)dst);
+    else *(u32x4 *)dst = v;
 }
 
 // Row-wide sum / max over the WPR waves of one row (LDS when WPR > 1).
@@ -410,7 +413,7 @@ __device__ __forceinline__ bool load_row(const typename RT<DT>::S *x, int n, int
     return full;
 }
 
-template <int VEC, int NCH, int WPR, typename OS, typename CT>
+template <int VEC, int NCH, int WPR, bool NT = false, typename OS, typename CT>
 __device__ __forceinline__ void store_row(OS *y, int n, int wr, int lane, bool full, const CT (&v)[NCH][VEC])
 {
 #pragma unroll
@@ -421,10 +424,10 @@ __device__ __forceinline__ void store_row(OS *y, int n, int wr, int lane, bool f
         for (int k = 0; k < VEC; k++) r[k] = (OS)v[c][k];
         if (full || i + VEC <= n) {
             if constexpr (VEC * sizeof(OS) == 16) {
-                store16(y + i, r);
+                store16<NT>(y + i, r);
             } else if constexpr (VEC * sizeof(OS) == 32) {
-                store16(y + i, r);
-                store16((char *)(y + i) + 16, (const char *)r + 16);
+                store16<NT>(y + i, r);
+                store16<NT>((char *)(y + i) + 16, (const char *)r + 16);
             } else {
 #pragma unroll
                 for (int k = 0; k < VEC; k++) y[i + k] = r[k];
@@ -481,7 +484,10 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
 
 // Fused softmax: y = exp(x - max) / sum(exp(x - max)), true division as the
 // composite's OP_DIV (cuda_array_ce.c:1995).  One HBM read, one write.
-template <int DT, int VEC, int NCH, int WPR, typename OS>
+// LNT / SNT: nontemporal row loads / stores.  RW: the grid walks the rows
+// (rows blockIdx.x, + gridDim.x, ...) and issues the next row's loads before
+// the current row's reductions, so HBM stays busy across its two passes.
+template <int DT, int VEC, int NCH, int WPR, typename OS, bool LNT = false, bool SNT = false, bool RW = false>
 __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xin, size_t rows,
                                                      int n, size_t ld, OS *__restrict__ out)
 {
@@ -490,35 +496,50 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
     __shared__ C lds[4];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6, wr = wave % WPR;
-    const size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
-    if (row >= rows) return;  // WPR > 1: one row per block, never taken
-    const S *x = (const S *)xin + row * ld;
-    OS *y = out + row * (size_t)n;
-    C v[NCH][VEC];
-    const bool full = load_row<DT, VEC, NCH, WPR, false>(x, n, wr, lane, neg_inf<C>(), v);
-    C m = neg_inf<C>();
+    size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    const size_t row_step = RW ? (size_t)gridDim.x * (4 / WPR) : rows;
+    if (row >= rows) return;  // WPR > 1: uniform per block
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    C nx[NCH][VEC];
+    if constexpr (RW) load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * ld, n, wr, lane, neg_inf<C>(), nx);
+    for (; row < rows; row += row_step) {
+        OS *y = out + row * (size_t)n;
+        C v[NCH][VEC];
+        if constexpr (RW) {
 #pragma unroll
-    for (int c = 0; c < NCH; c++)
+            for (int c = 0; c < NCH; c++)
 #pragma unroll
-        for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
-    m = row_max<C, WPR>(m, lds);
-    C sum = 0;
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        const int i = chunk_start<VEC, WPR>(c, wr, lane);
-#pragma unroll
-        for (int k = 0; k < VEC; k++) {
-            C e = (full || i + k < n) ? exp_c(v[c][k] - m) : (C)0;
-            v[c][k] = e;
-            sum = sum + e;
+                for (int k = 0; k < VEC; k++) v[c][k] = nx[c][k];
+            if (row + row_step < rows)
+                load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + (row + row_step) * ld, n, wr, lane, neg_inf<C>(),
+                                                 nx);
+        } else {
+            load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * ld, n, wr, lane, neg_inf<C>(), v);
         }
+        C m = neg_inf<C>();
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
+        m = row_max<C, WPR>(m, lds);
+        C sum = 0;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                C e = (full || i + k < n) ? exp_c(v[c][k] - m) : (C)0;
+                v[c][k] = e;
+                sum = sum + e;
+            }
+        }
+        sum = row_sum<C, WPR>(sum, lds);
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
+        store_row<VEC, NCH, WPR, SNT>(y, n, wr, lane, full, v);
     }
-    sum = row_sum<C, WPR>(sum, lds);
-#pragma unroll
-    for (int c = 0; c < NCH; c++)
-#pragma unroll
-        for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
-    store_row<VEC, NCH, WPR>(y, n, wr, lane, full, v);
 }
 
 // 16-byte-aligned vector load of VEC values (VEC * sizeof(T) a multiple of 16).
@@ -540,7 +561,7 @@ __device__ __forceinline__ void load_vec16(const T *p, T (&v)[VEC])
 // rows blockIdx.x, blockIdx.x + gridDim.x, ... and keeps its gamma / beta
 // chunks in registers across them, so they are read once per block instead
 // of once per row.
-template <int DT, int VEC, int NCH, int WPR, typename CT>
+template <int DT, int VEC, int NCH, int WPR, typename CT, bool LNT = false, bool SNT = false>
 __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ xin, size_t rows,
                                                        int n, CT eps, const CT *__restrict__ gamma,
                                                        const CT *__restrict__ beta,
@@ -573,7 +594,7 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
     // while two rows and gamma/beta fit the register budget)
     constexpr bool PF = NCH * VEC <= 32;
     CT nx[NCH][VEC];
-    if constexpr (PF) load_row<DT, VEC, NCH, WPR, false>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, nx);
+    if constexpr (PF) load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, nx);
     for (; row < rows; row += row_step) {
         CT *y = out + row * (size_t)n;
         CT v[NCH][VEC];
@@ -583,10 +604,10 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
 #pragma unroll
                 for (int k = 0; k < VEC; k++) v[c][k] = nx[c][k];
             if (row + row_step < rows)
-                load_row<DT, VEC, NCH, WPR, false>((const S *)xin + (row + row_step) * (size_t)n, n, wr, lane,
-                                                   (CT)0, nx);
+                load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + (row + row_step) * (size_t)n, n, wr, lane,
+                                                 (CT)0, nx);
         } else {
-            load_row<DT, VEC, NCH, WPR, false>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, v);
+            load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, v);
         }
         CT s = 0;
 #pragma unroll
@@ -617,7 +638,7 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
                 v[c][k] = t;
             }
         }
-        store_row<VEC, NCH, WPR>(y, n, wr, lane, full, v);
+        store_row<VEC, NCH, WPR, SNT>(y, n, wr, lane, full, v);
     }
 }
 

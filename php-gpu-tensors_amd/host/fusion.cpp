@@ -664,14 +664,27 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
     os << "extern \"C\" __global__ __launch_bounds__(256) void " << k.name << "_v(" << params;
     for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
     const int nd = k.ndims;
-    os << "){\nconst unsigned long long n4=" << k.total / 4 << "ULL;\n"
-       << "for(unsigned long long g=(unsigned long long)blockIdx.x*blockDim.x+threadIdx.x;g<n4;"
-          "g+=(unsigned long long)blockDim.x*gridDim.x){\n"
-       << "const unsigned long long i0=g*4ULL;\n";
+    // 32-bit index arithmetic (division by the constant extents becomes a
+    // multiply-high) when the element count and every leaf offset fit
+    bool i32 = k.total < (1ULL << 32);
+    for (const LeafMap &m : k.leaf_maps) {
+        long long reach = m.offset;
+        if (m.offset < 0) i32 = false;
+        for (int d = 0; d < nd; d++) {
+            if (m.stride[d] < 0) i32 = false;
+            reach += (long long)(k.shape[d] - 1) * m.stride[d];
+        }
+        if (reach >= (1LL << 32)) i32 = false;
+    }
+    const std::string IT = i32 ? "unsigned int" : "unsigned long long", SUF = i32 ? "U" : "ULL";
+    os << "){\nconst " << IT << " n4=" << k.total / 4 << SUF << ";\n"
+       << "for(" << IT << " g=(" << IT << ")blockIdx.x*blockDim.x+threadIdx.x;g<n4;"
+       << "g+=(" << IT << ")blockDim.x*gridDim.x){\n"
+       << "const " << IT << " i0=g*4" << SUF << ";\n";
     // coordinates of element i0
     unsigned long long div = 1;
     for (int d = nd - 1; d >= 0; d--) {
-        os << "const unsigned long long c" << d << "=(i0/" << div << "ULL)%" << k.shape[d] << "ULL;\n";
+        os << "const " << IT << " c" << d << "=(i0/" << div << SUF << ")%" << k.shape[d] << SUF << ";\n";
         div *= (unsigned long long)k.shape[d];
     }
     const char *f[4] = {"x", "y", "z", "w"};
@@ -682,9 +695,9 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
         const Tensor &t = *p.items[id].t;
         std::string st = storage_type(t.dtype);
         std::string L = "L" + std::to_string(l);
-        os << "const unsigned long long o" << l << "=" << m.offset << "ULL";
+        os << "const " << IT << " o" << l << "=" << m.offset << SUF;
         for (int d = 0; d < nd; d++)
-            if (m.stride[d]) os << "+c" << d << "*" << m.stride[d] << "ULL";
+            if (m.stride[d]) os << "+c" << d << "*" << m.stride[d] << SUF;
         os << ";\n";
         std::string base = "static_cast<const " + st + "*>(p" + std::to_string(l) + ")";
         std::string at = base + "+o" + std::to_string(l);
@@ -712,7 +725,7 @@ static void emit_vector(Plan &p, Kernel &k, std::ostringstream &os)
         } else {
             for (int j = 0; j < 4; j++)
                 os << "const " << ctype(t.dtype) << " " << L << "_" << j << "="
-                   << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j * inner) + "ULL]")
+                   << load_conv(t.dtype, base + "[o" + std::to_string(l) + "+" + std::to_string(j * inner) + SUF + "]")
                    << ";\n";
         }
     }

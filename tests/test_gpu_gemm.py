@@ -142,6 +142,34 @@ def test_matmul_direct_lds_kernel(A, dt, layout, bmnk):
         A.load().pt_matmul_set_tile(-1)
 
 
+@pytest.mark.parametrize("tile", list(range(14, 24)))
+@pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("layout", ["NN", "NT"])
+@pytest.mark.parametrize("bmnk", [(2, 512, 256, 512), (1, 256, 512, 384), (3, 256, 256, 128),
+                                  (1, 256, 256, 96), (1, 512, 384, 256)], ids=str)
+def test_matmul_ring_kernel(A, tile, dt, layout, bmnk):
+    """Tiles 14-23 (k_gemm_ring: K step x stages x tile width x schedule):
+    exact on integer-valued operands for row-major and k-contiguous B,
+    including K-step counts that are not a multiple of the stage count
+    (384 / 32 = 12 steps on the 5-stage ring, 128 / 32 = 4 < 5 steps) and
+    shapes the ring does not take (K = 96, N = 384 for 256-wide tiles),
+    which run the fallback tiles."""
+    A.load().pt_matmul_set_tile(tile)
+    try:
+        b_, m, n, k = bmnk
+        a = O.to_storage(_ints((b_, m, k), seed=m + 3 * k), dt)
+        b = O.to_storage(_ints((b_, k, n), seed=n + 5 * k), dt)
+        expect = ref(a, b, dt)
+        kw = {}
+        b_in = b
+        if layout == "NT":
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+            kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
+        assert np.array_equal(run(A, a, b_in, dt, **kw), expect)
+    finally:
+        A.load().pt_matmul_set_tile(-1)
+
+
 def test_matmul_direct_lds_batch_broadcast(A):
     A.load().pt_matmul_set_tile(8)
     try:
