@@ -177,6 +177,19 @@ pt_status pt_reduce(const void *input, void *output, int dtype, int op,
 /* Output dtype pt_reduce writes for (dtype, op); -1 if unsupported. */
 int pt_reduce_result_dtype(int dtype, int op);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same arguments, kernels and results as pt_reduce,
+ * but the scratch those kernels use (global-reduction partials,
+ * column-split partials, the packed copy of a strided input) comes from a
+ * static 1 MiB buffer the library holds on each device, not from the pool;
+ * nothing is allocated.  A reduction that needs more scratch fails with
+ * PT_ERR_INVALID.  Every call on a device shares that device's buffer:
+ * calls that overlap on one device (other threads or streams) race. */
+pt_status pt_reduce_noalloc(const void *input, void *output, int dtype, int op,
+                            const int *shape, const size_t *strides, int ndims, int axis,
+                            size_t base_offset, pt_stream_t stream);
+
 /* Replaces launch_arg_reduction (reduction_ops.h:31-38): int32 indices of
  * the max/min along axis (axis < 0: flattened), ties -> lowest index, NaN
  * never selected, an axis whose best value equals the identity -> 0

@@ -21,6 +21,10 @@ hipStream_t stream_of(pt_stream_t s);
 pt_status ensure_init();
 pt_status scratch_alloc(void **ptr, size_t bytes, hipStream_t stream);
 void scratch_free(void *ptr, hipStream_t stream);
+// static scratch of the no-allocation entry points (1 MiB per device)
+#define PT_STATIC_SCRATCH_BYTES (1u << 20)
+pt_status static_scratch_begin();
+void static_scratch_end();
 pt_backend_info &counters();
 
 #define PT_TRY(expr)                      \

@@ -1700,6 +1700,21 @@ pt_status pt_reduce(const void *input, void *output, int dtype, int op,
                          axis, base_offset, 0, 0, stream);
 }
 
+pt_status pt_reduce_noalloc(const void *input, void *output, int dtype, int op,
+                            const int *shape, const size_t *strides, int ndims, int axis,
+                            size_t base_offset, pt_stream_t stream)
+{
+    int rop = red_op_of(op);
+    if (rop < 0 || rop == R_ARGMAX || rop == R_ARGMIN)
+        return fail(PT_ERR_INVALID, "pt_reduce_noalloc: unsupported op %d", op);
+    PT_TRY(ensure_init());
+    PT_TRY(static_scratch_begin());
+    pt_status st = reduce_driver(input, output, dtype, rop, result_dtype(dtype, rop), shape, strides, ndims,
+                                 axis, base_offset, 0, 0, stream);
+    static_scratch_end();
+    return st;
+}
+
 pt_status pt_arg_reduce(const void *input, int32_t *output, int dtype, int op,
                         const int *shape, const size_t *strides, int ndims, int axis,
                         size_t base_offset, pt_stream_t stream)

@@ -99,6 +99,32 @@ hipStream_t stream_of(pt_stream_t s)
     return s ? (hipStream_t)s : (t_current ? t_current : g_stream);
 }
 
+// Static scratch of the no-allocation entry points (pt_reduce_noalloc): a
+// file-scope device array that every GPU the library runs on holds for the
+// life of the process.  Host code never uses the array's name as an
+// address: its device address is looked up per device with
+// hipGetSymbolAddress (with that device current) the first time an entry
+// point runs there.
+static __device__ __align__(256) unsigned char scratch[PT_STATIC_SCRATCH_BYTES];
+static std::mutex g_static_mu;
+static void *g_static_ptr[64];
+
+pt_status static_scratch_address(void **ptr)
+{
+    int dev = 0;
+    PT_TRY(check_hip(hipGetDevice(&dev), "hipGetDevice"));
+    if (dev < 0 || dev >= 64) return fail(PT_ERR_RUNTIME, "device %d outside the static scratch table", dev);
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    if (!g_static_ptr[dev]) {
+        void *p = nullptr;
+        PT_TRY(check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address"));
+        if (!p) return fail(PT_ERR_RUNTIME, "static scratch has no device address");
+        g_static_ptr[dev] = p;
+    }
+    *ptr = g_static_ptr[dev];
+    return PT_OK;
+}
+
 // Scratch of the multi-kernel operations (split-K partials, column and
 // global reduction partials).  By default it comes from the stream-ordered
 // pool.  Between pt_workspace_begin and pt_workspace_end it is carved from
@@ -106,8 +132,10 @@ hipStream_t stream_of(pt_stream_t s)
 // before it returns), so that a captured HIP graph holds no allocation; in
 // measuring mode (no arena) it still comes from the pool and the peak is
 // recorded, which sizes the arena.
+// Between static_scratch_begin and static_scratch_end the arena is the
+// device's static scratch (`fixed`: never the pool).
 struct Workspace {
-    bool active = false, measure = false;
+    bool active = false, measure = false, fixed = false;
     char *base = nullptr;
     size_t bytes = 0, top = 0, peak = 0;
     std::vector<std::pair<void *, size_t>> stack;
@@ -120,6 +148,15 @@ pt_status scratch_alloc(void **ptr, size_t bytes, hipStream_t stream)
 {
     if (!t_ws.active) return check_hip(hipMallocAsync(ptr, bytes ? bytes : 1, stream), "scratch allocation");
     const size_t need = ws_round(bytes ? bytes : 1);
+    if (t_ws.fixed) {
+        // static scratch: a bump pointer, nothing allocated (not even host memory)
+        if (t_ws.top + need > t_ws.bytes)
+            return fail(PT_ERR_INVALID, "operation needs %zu bytes of scratch; the static scratch holds %zu",
+                        t_ws.top + need, t_ws.bytes);
+        *ptr = t_ws.base + t_ws.top;
+        t_ws.top += need;
+        return PT_OK;
+    }
     if (t_ws.measure) {
         PT_TRY(check_hip(hipMallocAsync(ptr, need, stream), "scratch allocation"));
     } else {
@@ -140,6 +177,7 @@ void scratch_free(void *ptr, hipStream_t stream)
         (void)hipFreeAsync(ptr, stream);
         return;
     }
+    if (t_ws.fixed) return;  // static scratch: released by static_scratch_end
     for (size_t i = t_ws.stack.size(); i-- > 0;) {
         if (t_ws.stack[i].first != ptr) continue;
         if (t_ws.measure) (void)hipFreeAsync(ptr, stream);
@@ -149,6 +187,27 @@ void scratch_free(void *ptr, hipStream_t stream)
         t_ws.stack.erase(t_ws.stack.begin() + (long)i);
         return;
     }
+}
+
+// Scratch of the calls between static_scratch_begin and static_scratch_end
+// comes from the device's static scratch array (a stack, as a workspace);
+// a request beyond it fails with PT_ERR_INVALID instead of allocating.
+pt_status static_scratch_begin()
+{
+    if (t_ws.active) return fail(PT_ERR_INVALID, "a workspace is already active on this thread");
+    void *p = nullptr;
+    PT_TRY(static_scratch_address(&p));
+    t_ws = Workspace();
+    t_ws.active = true;
+    t_ws.fixed = true;
+    t_ws.base = (char *)p;
+    t_ws.bytes = PT_STATIC_SCRATCH_BYTES;
+    return PT_OK;
+}
+
+void static_scratch_end()
+{
+    t_ws = Workspace();
 }
 
 }  // namespace pt

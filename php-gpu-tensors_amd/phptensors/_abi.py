@@ -101,6 +101,8 @@ SIGNATURES = {
     "pt_reduce": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, c_int_p, c_size_p,
                                  ctypes.c_int, ctypes.c_int, ctypes.c_size_t, vp]),
     "pt_reduce_result_dtype": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
+    "pt_reduce_noalloc": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, c_int_p, c_size_p,
+                                         ctypes.c_int, ctypes.c_int, ctypes.c_size_t, vp]),
     "pt_arg_reduce": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, c_int_p, c_size_p,
                                      ctypes.c_int, ctypes.c_int, ctypes.c_size_t, vp]),
     "pt_moments": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, c_int_p, c_size_p,
