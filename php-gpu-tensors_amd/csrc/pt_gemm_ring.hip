@@ -104,10 +104,15 @@ constexpr int stages_per_base(int stage_bytes, int max_inner)
 // BN: 256 (4 x 4 blocks per wave, one workgroup per CU) or 128 (4 x 2
 // blocks per wave, WGS = 2 workgroups per CU, whose barriers and load
 // waits then overlap each other's MFMAs).
-// ILV: one fragment read (and, after the barrier, one load-to-LDS) between
+// ILV 1: one fragment read (and, after the barrier, one load-to-LDS) between
 // consecutive MFMAs instead of each group in one burst, so that a read
 // waiting for the LDS queue never holds back the MFMAs behind it.
-template <int DT, bool B_KC, int BK, int NST, int BN, int WGS, bool ILV>
+// ILV 2: as 1, and the loads of step k + NST - 1 are spread evenly over all
+// of step k's MFMAs (into the stage freed by step k-1's barrier) rather
+// than issued together after a barrier: four waves issuing their loads at
+// once fill the CU's address queue, and in-order issue then holds every
+// MFMA behind a load (needs NST >= 3 for the loads to land in time).
+template <int DT, bool B_KC, int BK, int NST, int BN, int WGS, int ILV>
 __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
 {
     using S = uint16_t;
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
     constexpr int GROUP_M = 4;
     constexpr bool kGuard = (NST & (NST - 1)) != 0;
     static_assert(NS % 2 == 0 && NST >= 2 && NST <= 8 && (NST - 1) * PER < 64, "pipeline shape");
+    static_assert(ILV != 2 || (NST >= 3 && (NS * TM * TN) % PER == 0), "spread loads need three stages");
     static_assert(NQA >= 1 && NQB >= 1 && (BN == 256 || BN == 128), "load split");
     // All stages of an operand in one array.  Fragment reads are inline asm
     // from a per-lane base register plus an instruction offset (16 bits), so
@@ -309,11 +315,25 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
     };
 
     const int KT = g.K / BK;
-    // steps 0 .. NST-1 fill the ring; step 0 is needed first, NST-1 steps
-    // of loads may stay in flight
-    static_for<0, NST>([&](auto P) { issue(min((int)decltype(P)::value, KT - 1), P); });
-    ring_wait<(NST - 1) * PER>();
+    // the ring starts with steps 0 .. NST-1 (spread schedule: 0 .. NST-2,
+    // step NST-1 follows during step 0); step 0 is needed first
+    constexpr int PRO = ILV == 2 ? NST - 1 : NST;
+    static_for<0, PRO>([&](auto P) { issue(min((int)decltype(P)::value, KT - 1), P); });
+    ring_wait<(PRO - 1) * PER>();
     ring_barrier();
+    // spread schedule: the load issued at MFMA q of slice sl of step kt
+    constexpr int SPREAD = ILV == 2 ? NS * TM * TN / PER : 1;
+    // loads issued after step kt+1's when step kt's barrier is reached: steps
+    // kt+2 .. kt+NST-1 whole, or (spread) steps kt+2 .. kt+NST-2 whole plus the
+    // loads of step kt+NST-1 placed in slices 0 .. NS-2 of step kt
+    constexpr int WAIT_STEP = ILV == 2 ? (NST - 3) * PER + (NS - 1) * TM * TN / SPREAD : (NST - 2) * PER;
+    auto spread_load = [&](int kt, auto J, auto SL, auto Q) {
+        if constexpr (ILV == 2) {
+            constexpr int slot = decltype(SL)::value * TM * TN + decltype(Q)::value;
+            if constexpr (slot % SPREAD == 0)
+                issue_one(min(kt + NST - 1, KT - 1), IC<decltype(J)::value + NST - 1>{}, IC<slot / SPREAD>{});
+        }
+    };
     Frag fa[2][TM], fb[2][TN];
     read_frags(IC<0>{}, IC<0>{}, fa[0], fb[0]);
     frag_wait(fa[0], fb[0]);
@@ -330,6 +350,7 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
                         static_for<0, TM * TN>([&](auto Q) {
                             mfma_one(Q, fa[c], fb[c]);
                             if constexpr (decltype(Q)::value < TM + TN) read_one(J, IC<sl + 1>{}, Q, fa[n], fb[n]);
+                            spread_load(kt, J, SL, Q);
                             __builtin_amdgcn_sched_barrier(0);
                         });
                     } else {
@@ -339,10 +360,17 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
                     }
                     frag_wait(fa[n], fb[n]);
                 });
-                ring_wait<(NST - 2) * PER>();  // this wave's loads of step kt+1 landed
+                ring_wait<WAIT_STEP>();  // this wave's loads of step kt+1 landed
                 ring_barrier();                // ... everyone's; step kt's stage is free
                 const int knext = min(kt + NST, KT - 1);
-                if constexpr (ILV) {
+                if constexpr (ILV == 2) {
+                    static_for<0, TM * TN>([&](auto Q) {
+                        mfma_one(Q, fa[1], fb[1]);
+                        if constexpr (decltype(Q)::value < TM + TN) read_one(IC<j + 1>{}, IC<0>{}, Q, fa[0], fb[0]);
+                        spread_load(kt, J, IC<NS - 1>{}, Q);
+                        __builtin_amdgcn_sched_barrier(0);
+                    });
+                } else if constexpr (ILV) {
                     constexpr int QN = TM * TN > PER ? TM * TN : PER;
                     static_for<0, QN>([&](auto Q) {
                         constexpr int q = decltype(Q)::value;
@@ -392,10 +420,11 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
         }
 }
 
-// Ring shapes: {BK, stages, BN, workgroups per CU, interleaved schedule}
+// Ring shapes: {BK, stages, BN, workgroups per CU, schedule}
 static const int kRing[][5] = {{32, 4, 256, 1, 0}, {64, 2, 256, 1, 0}, {32, 2, 256, 1, 0}, {32, 3, 256, 1, 0},
                                {32, 5, 256, 1, 0}, {32, 3, 128, 2, 0}, {32, 2, 128, 2, 0}, {64, 2, 256, 1, 1},
-                               {32, 4, 256, 1, 1}, {32, 3, 128, 2, 1}};
+                               {32, 4, 256, 1, 1}, {32, 3, 128, 2, 1}, {32, 4, 256, 1, 2}, {32, 3, 256, 1, 2},
+                               {32, 5, 256, 1, 2}};
 
 int gemm_ring_variants() { return (int)(sizeof(kRing) / sizeof(kRing[0])); }
 int gemm_ring_bn(int variant) { return kRing[variant][2]; }
@@ -410,24 +439,27 @@ int gemm_ring_kmul(int variant)
 void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s)
 {
     const dim3 block(256);
-#define PT_RING(DTV, BKV, STV, BNV, WGV, ILV)                                                  \
-    do {                                                                                       \
-        if (b_row) k_gemm_ring<DTV, false, BKV, STV, BNV, WGV, ILV><<<grid, block, 0, s>>>(g); \
-        else k_gemm_ring<DTV, true, BKV, STV, BNV, WGV, ILV><<<grid, block, 0, s>>>(g);        \
+#define PT_RING(DTV, BKV, STV, BNV, WGV, ILVV)                                                  \
+    do {                                                                                        \
+        if (b_row) k_gemm_ring<DTV, false, BKV, STV, BNV, WGV, ILVV><<<grid, block, 0, s>>>(g); \
+        else k_gemm_ring<DTV, true, BKV, STV, BNV, WGV, ILVV><<<grid, block, 0, s>>>(g);        \
     } while (0)
 #define PT_RING_DT(DTV)                                                                        \
     do {                                                                                       \
         switch (variant) {                                                                     \
-        case 0: PT_RING(DTV, 32, 4, 256, 1, false); break;                                     \
-        case 1: PT_RING(DTV, 64, 2, 256, 1, false); break;                                     \
-        case 2: PT_RING(DTV, 32, 2, 256, 1, false); break;                                     \
-        case 3: PT_RING(DTV, 32, 3, 256, 1, false); break;                                     \
-        case 4: PT_RING(DTV, 32, 5, 256, 1, false); break;                                     \
-        case 5: PT_RING(DTV, 32, 3, 128, 2, false); break;                                     \
-        case 6: PT_RING(DTV, 32, 2, 128, 2, false); break;                                     \
-        case 7: PT_RING(DTV, 64, 2, 256, 1, true); break;                                      \
-        case 8: PT_RING(DTV, 32, 4, 256, 1, true); break;                                      \
-        default: PT_RING(DTV, 32, 3, 128, 2, true); break;                                     \
+        case 0: PT_RING(DTV, 32, 4, 256, 1, 0); break;                                         \
+        case 1: PT_RING(DTV, 64, 2, 256, 1, 0); break;                                         \
+        case 2: PT_RING(DTV, 32, 2, 256, 1, 0); break;                                         \
+        case 3: PT_RING(DTV, 32, 3, 256, 1, 0); break;                                         \
+        case 4: PT_RING(DTV, 32, 5, 256, 1, 0); break;                                         \
+        case 5: PT_RING(DTV, 32, 3, 128, 2, 0); break;                                         \
+        case 6: PT_RING(DTV, 32, 2, 128, 2, 0); break;                                         \
+        case 7: PT_RING(DTV, 64, 2, 256, 1, 1); break;                                         \
+        case 8: PT_RING(DTV, 32, 4, 256, 1, 1); break;                                         \
+        case 9: PT_RING(DTV, 32, 3, 128, 2, 1); break;                                         \
+        case 10: PT_RING(DTV, 32, 4, 256, 1, 2); break;                                        \
+        case 11: PT_RING(DTV, 32, 3, 256, 1, 2); break;                                        \
+        default: PT_RING(DTV, 32, 5, 256, 1, 2); break;                                        \
         }                                                                                      \
     } while (0)
     if (dtype == PT_BFLOAT16) PT_RING_DT(PT_BFLOAT16);
