@@ -690,13 +690,13 @@ enum GemmTile {
     TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_128x128_W8_K2 = 11,
     TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13,
     // 4-wave LDS-ring kernels (k_gemm_ring): BK x stages
-    TILE_RING_FIRST = 14, TILE_RING_LAST = 26,  // variants 0..12 of gemm_ring_variants()
-    TILE_COUNT = 27,
-    // large bf16 products: BK 32, five stages, loads spread over the MFMA
-    // slices (the fastest shape measured on config 4: 606 us against 620 us
-    // for BK 64 x two stages, 694 us for the direct kernel); large fp16
-    // products keep the direct kernel, which measured 1% ahead of every ring
-    TILE_RING_DEFAULT = TILE_RING_FIRST + 12
+    TILE_RING_FIRST = 14, TILE_RING_LAST = 31,  // variants 0..17 of gemm_ring_variants()
+    TILE_COUNT = 32,
+    // large bf16 products: 4 waves, BK 32, five stages, loads spread over
+    // the MFMA slices (606 us on config 4 against 620 us for BK 64 x two
+    // stages and 693 us for the direct kernel); large fp16 products: the same
+    // ring with 8 waves (673 us against 701 us with 4 waves, 706 us direct)
+    TILE_RING_DEFAULT = TILE_RING_FIRST + 12, TILE_RING_DEFAULT_F16 = TILE_RING_FIRST + 16
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
@@ -704,7 +704,8 @@ static const TileInfo kTiles[TILE_COUNT] = {
     {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}, {128, 128, 2},
     {128, 64, 1}, {128, 64, 2}, {256, 256, 1}, {256, 256, 2}, {256, 256, 1}, {256, 256, 1},
     {256, 256, 1}, {256, 128, 1}, {256, 128, 1}, {256, 256, 2}, {256, 256, 1}, {256, 128, 1},
-    {256, 256, 1}, {256, 256, 1}, {256, 256, 1}};
+    {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1},
+    {256, 256, 1}, {256, 256, 1}};
 
 static int g_tile_override = -1;
 
@@ -906,7 +907,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         const int mid32 = g.b_sn == 1 ? TILE_128x128_W8 : TILE_128x64_W4M2;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
                    ? (dtype == PT_FLOAT32 ? TILE_256x128_W8
-                      : dtype == PT_BFLOAT16 ? TILE_RING_DEFAULT : TILE_256x256_DIRECT)
+                      : dtype == PT_BFLOAT16 ? TILE_RING_DEFAULT : TILE_RING_DEFAULT_F16)
                    : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? mid32 : TILE_128x128)
                                                 : TILE_64x64;
     }
@@ -1075,7 +1076,7 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
                                 TILE_128x64_W4M2_K2};
     static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
                                 TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8, TILE_RING_DEFAULT,
-                                TILE_RING_FIRST + 7, TILE_RING_FIRST + 8};
+                                TILE_RING_DEFAULT_F16, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};
     const int *cands = dtype == PT_FLOAT32 ? kFp32 : kHalf;
     const int ncand = dtype == PT_FLOAT32 ? (int)(sizeof(kFp32) / sizeof(int)) : (int)(sizeof(kHalf) / sizeof(int));
     hipStream_t s = stream_of(stream);

@@ -1,13 +1,14 @@
-// 4-wave LDS-ring GEMM kernel for bf16 / fp16 on gfx950 (see the comment
-// block below).  Launched by pt_matmul (pt_gemm.hip) through
-// launch_gemm_ring.
+// LDS-ring GEMM kernel for bf16 / fp16 on gfx950, 4 or 8 waves per 256-row
+// tile (see the comment blocks below).  Launched by pt_matmul (pt_gemm.hip)
+// through launch_gemm_ring.
 #include "pt_gemm.h"
 
 namespace pt {
 
-// ------------------------------------------ 4-wave LDS-ring 16-bit kernel
+// ------------------------------------------------ LDS-ring 16-bit kernel
 // bf16 / fp16 GEMM for whole 256x256 tiles, K a multiple of BK * NST,
-// k-contiguous A, B k- or n-contiguous.  Four waves in a 2 x 2 grid, each
+// k-contiguous A, B k- or n-contiguous.  Four waves in a 2 x 2 grid (the
+// 8-wave form is described at the template), each
 // owning a 128 x 128 sub-tile: 4 x 4 blocks of 32 x 32, i.e. 256 fp32
 // accumulators per lane.  At one workgroup per CU a wave has its SIMD's
 // whole register file, so the accumulators live in the accumulation
@@ -112,18 +113,23 @@ constexpr int stages_per_base(int stage_bytes, int max_inner)
 // than issued together after a barrier: four waves issuing their loads at
 // once fill the CU's address queue, and in-order issue then holds every
 // MFMA behind a load (needs NST >= 3 for the loads to land in time).
-template <int DT, bool B_KC, int BK, int NST, int BN, int WGS, int ILV>
-__global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
+// NW: 4 waves (2 x 2, 128 x 128 each) or 8 waves (2 x 4, 128 x 64 each: two
+// waves per SIMD with 128 accumulators apiece, so that one wave's MFMAs run
+// while the other waits to issue a load or at a barrier; 6 fragment reads
+// per 8 MFMAs instead of 8 per 16).
+template <int DT, bool B_KC, int BK, int NST, int BN, int WGS, int ILV, int NW>
+__global__ __launch_bounds__(64 * NW, WGS) void k_gemm_ring(GemmArgs g)
 {
     using S = uint16_t;
-    constexpr int BM = 256, WTM = 128, WTN = BN / 2, TM = 4, TN = WTN / 32;
+    constexpr int WGN = NW / 2;            // wave grid: 2 x WGN
+    constexpr int BM = 256, WTM = 128, WTN = BN / WGN, TM = 4, TN = WTN / 32;
     constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
     constexpr int CPR = BK / 8;            // 16-byte chunks per k-contiguous row
     constexpr int RPI = 64 / CPR;          // such rows per load instruction (64 lanes x 16 B)
     constexpr int CPB = BN / 8;            // 16-byte chunks per k-row of row-major B
     constexpr int KPI = 64 / CPB;          // k-rows of row-major B per load instruction
-    constexpr int NQA = A_ELEMS / 512 / 4; // load instructions per wave and step: A
-    constexpr int NQB = B_ELEMS / 512 / 4; // ... and B
+    constexpr int NQA = A_ELEMS / 512 / NW; // load instructions per wave and step: A
+    constexpr int NQB = B_ELEMS / 512 / NW; // ... and B
     constexpr int PER = NQA + NQB;         // vmcnt units per step
     constexpr int NS = BK / 16;            // MFMA k-slices per step
     constexpr int GROUP_M = 4;
@@ -131,6 +137,7 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
     static_assert(NS % 2 == 0 && NST >= 2 && NST <= 8 && (NST - 1) * PER < 64, "pipeline shape");
     static_assert(ILV != 2 || (NST >= 3 && (NS * TM * TN) % PER == 0), "spread loads need three stages");
     static_assert(NQA >= 1 && NQB >= 1 && (BN == 256 || BN == 128), "load split");
+    static_assert((NW == 4 || NW == 8) && (TN == 2 || TN == 4), "wave grid");
     // All stages of an operand in one array.  Fragment reads are inline asm
     // from a per-lane base register plus an instruction offset (16 bits), so
     // the compiler neither sees them as LDS reads (it would make them wait
@@ -167,7 +174,7 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
     const long long lda = g.a_sm, ldb = B_KC ? g.b_sn : g.b_sk;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WGN, wn = wave % WGN;
 
     // per-lane source offsets of each load instruction, without the k step
     long long offa[NQA], offb[NQB];
@@ -420,11 +427,13 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_ring(GemmArgs g)
         }
 }
 
-// Ring shapes: {BK, stages, BN, workgroups per CU, schedule}
-static const int kRing[][5] = {{32, 4, 256, 1, 0}, {64, 2, 256, 1, 0}, {32, 2, 256, 1, 0}, {32, 3, 256, 1, 0},
-                               {32, 5, 256, 1, 0}, {32, 3, 128, 2, 0}, {32, 2, 128, 2, 0}, {64, 2, 256, 1, 1},
-                               {32, 4, 256, 1, 1}, {32, 3, 128, 2, 1}, {32, 4, 256, 1, 2}, {32, 3, 256, 1, 2},
-                               {32, 5, 256, 1, 2}};
+// Ring shapes: {BK, stages, BN, workgroups per CU, schedule, waves}
+static const int kRing[][6] = {{32, 4, 256, 1, 0, 4}, {64, 2, 256, 1, 0, 4}, {32, 2, 256, 1, 0, 4},
+                               {32, 3, 256, 1, 0, 4}, {32, 5, 256, 1, 0, 4}, {32, 3, 128, 2, 0, 4},
+                               {32, 2, 128, 2, 0, 4}, {64, 2, 256, 1, 1, 4}, {32, 4, 256, 1, 1, 4},
+                               {32, 3, 128, 2, 1, 4}, {32, 4, 256, 1, 2, 4}, {32, 3, 256, 1, 2, 4},
+                               {32, 5, 256, 1, 2, 4}, {32, 4, 256, 1, 1, 8}, {64, 2, 256, 1, 1, 8},
+                               {32, 4, 256, 1, 2, 8}, {32, 5, 256, 1, 2, 8}, {32, 3, 256, 1, 2, 8}};
 
 int gemm_ring_variants() { return (int)(sizeof(kRing) / sizeof(kRing[0])); }
 int gemm_ring_bn(int variant) { return kRing[variant][2]; }
@@ -438,28 +447,33 @@ int gemm_ring_kmul(int variant)
 
 void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s)
 {
-    const dim3 block(256);
-#define PT_RING(DTV, BKV, STV, BNV, WGV, ILVV)                                                  \
-    do {                                                                                        \
-        if (b_row) k_gemm_ring<DTV, false, BKV, STV, BNV, WGV, ILVV><<<grid, block, 0, s>>>(g); \
-        else k_gemm_ring<DTV, true, BKV, STV, BNV, WGV, ILVV><<<grid, block, 0, s>>>(g);        \
+    const dim3 block(64 * kRing[variant][5]);
+#define PT_RING(DTV, BKV, STV, BNV, WGV, ILVV, NWV)                                                    \
+    do {                                                                                               \
+        if (b_row) k_gemm_ring<DTV, false, BKV, STV, BNV, WGV, ILVV, NWV><<<grid, block, 0, s>>>(g);   \
+        else k_gemm_ring<DTV, true, BKV, STV, BNV, WGV, ILVV, NWV><<<grid, block, 0, s>>>(g);          \
     } while (0)
 #define PT_RING_DT(DTV)                                                                        \
     do {                                                                                       \
         switch (variant) {                                                                     \
-        case 0: PT_RING(DTV, 32, 4, 256, 1, 0); break;                                         \
-        case 1: PT_RING(DTV, 64, 2, 256, 1, 0); break;                                         \
-        case 2: PT_RING(DTV, 32, 2, 256, 1, 0); break;                                         \
-        case 3: PT_RING(DTV, 32, 3, 256, 1, 0); break;                                         \
-        case 4: PT_RING(DTV, 32, 5, 256, 1, 0); break;                                         \
-        case 5: PT_RING(DTV, 32, 3, 128, 2, 0); break;                                         \
-        case 6: PT_RING(DTV, 32, 2, 128, 2, 0); break;                                         \
-        case 7: PT_RING(DTV, 64, 2, 256, 1, 1); break;                                         \
-        case 8: PT_RING(DTV, 32, 4, 256, 1, 1); break;                                         \
-        case 9: PT_RING(DTV, 32, 3, 128, 2, 1); break;                                         \
-        case 10: PT_RING(DTV, 32, 4, 256, 1, 2); break;                                        \
-        case 11: PT_RING(DTV, 32, 3, 256, 1, 2); break;                                        \
-        default: PT_RING(DTV, 32, 5, 256, 1, 2); break;                                        \
+        case 0: PT_RING(DTV, 32, 4, 256, 1, 0, 4); break;                                      \
+        case 1: PT_RING(DTV, 64, 2, 256, 1, 0, 4); break;                                      \
+        case 2: PT_RING(DTV, 32, 2, 256, 1, 0, 4); break;                                      \
+        case 3: PT_RING(DTV, 32, 3, 256, 1, 0, 4); break;                                      \
+        case 4: PT_RING(DTV, 32, 5, 256, 1, 0, 4); break;                                      \
+        case 5: PT_RING(DTV, 32, 3, 128, 2, 0, 4); break;                                      \
+        case 6: PT_RING(DTV, 32, 2, 128, 2, 0, 4); break;                                      \
+        case 7: PT_RING(DTV, 64, 2, 256, 1, 1, 4); break;                                      \
+        case 8: PT_RING(DTV, 32, 4, 256, 1, 1, 4); break;                                      \
+        case 9: PT_RING(DTV, 32, 3, 128, 2, 1, 4); break;                                      \
+        case 10: PT_RING(DTV, 32, 4, 256, 1, 2, 4); break;                                     \
+        case 11: PT_RING(DTV, 32, 3, 256, 1, 2, 4); break;                                     \
+        case 12: PT_RING(DTV, 32, 5, 256, 1, 2, 4); break;                                     \
+        case 13: PT_RING(DTV, 32, 4, 256, 1, 1, 8); break;                                     \
+        case 14: PT_RING(DTV, 64, 2, 256, 1, 1, 8); break;                                     \
+        case 15: PT_RING(DTV, 32, 4, 256, 1, 2, 8); break;                                     \
+        case 16: PT_RING(DTV, 32, 5, 256, 1, 2, 8); break;                                     \
+        default: PT_RING(DTV, 32, 3, 256, 1, 2, 8); break;                                      \
         }                                                                                      \
     } while (0)
     if (dtype == PT_BFLOAT16) PT_RING_DT(PT_BFLOAT16);
@@ -468,4 +482,4 @@ void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim
 #undef PT_RING
 }
 
-}  // namespace pt
+} // namespace pt

@@ -142,13 +142,14 @@ def test_matmul_direct_lds_kernel(A, dt, layout, bmnk):
         A.load().pt_matmul_set_tile(-1)
 
 
-@pytest.mark.parametrize("tile", list(range(14, 24)))
+@pytest.mark.parametrize("tile", list(range(14, 32)))
 @pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "NT"])
 @pytest.mark.parametrize("bmnk", [(2, 512, 256, 512), (1, 256, 512, 384), (3, 256, 256, 128),
                                   (1, 256, 256, 96), (1, 512, 384, 256)], ids=str)
 def test_matmul_ring_kernel(A, tile, dt, layout, bmnk):
-    """Tiles 14-23 (k_gemm_ring: K step x stages x tile width x schedule):
+    """Tiles 14-31 (k_gemm_ring: K step x stages x tile width x schedule x
+    waves):
     exact on integer-valued operands for row-major and k-contiguous B,
     including K-step counts that are not a multiple of the stage count
     (384 / 32 = 12 steps on the 5-stage ring, 128 / 32 = 4 < 5 steps) and
