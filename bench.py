@@ -42,13 +42,14 @@ HBM_PEAK_GBS = 8000.0
 
 # HBM bytes per dispatch of each timed kernel: rocprofv3 --pmc FETCH_SIZE and
 # --pmc WRITE_SIZE passes over this script (--no-cpu --copy-calibration
-# --steps 2 --warmup 1), each scaled by what the counter reads for a 128 MiB
-# device copy (fetch x 2.0, write x 1.0).  Re-measured when a kernel changes.
+# --steps 2 --warmup 1 --only reduce,fused,gemm), each scaled by what the
+# counter reads for a 128 MiB device copy (fetch x 2.0, write x 1.0).
+# Re-measured when a kernel changes.
 PMC_TRAFFIC_BYTES = {
-    "reduce:sum": 134_509_568, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
-    "reduce:argmax": 134_530_048, "reduce:var": 134_534_144, "reduce:softmax": 268_549_120,
-    "reduce:layernorm": 269_134_848, "fused:tanh_x_plus_y_z": 1_610_682_048,
-    "gemm:bf16": 1_087_413_760, "gemm:fp16": 1_079_442_176, "gemm:fp32": 2_684_529_792,
+    "reduce:sum": 134_516_736, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
+    "reduce:argmax": 134_521_856, "reduce:var": 134_540_288, "reduce:softmax": 268_551_168,
+    "reduce:layernorm": 269_128_704, "fused:tanh_x_plus_y_z": 1_610_680_832,
+    "gemm:bf16": 1_078_037_184, "gemm:fp16": 1_083_219_328, "gemm:fp32": 2_684_526_208,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol
@@ -320,6 +321,48 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
     return fam
 
 
+# torch.bmm on the config-4 operands (hipBLASLt / rocBLAS through PyTorch):
+# a comparison point on the same box, run in a child process so that the
+# library and torch never share one process.  Not the product path.
+_VENDOR_GEMM = r"""
+import json, torch
+bsz, m, n, k = 32, 2048, 2048, 2048
+g = torch.Generator(device="cuda").manual_seed(4)
+out = {}
+for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16), ("fp32", torch.float32)):
+    a = (torch.randn(bsz, m, k, device="cuda", generator=g) * 0.02).to(dt).contiguous()
+    b = (torch.randn(bsz, k, n, device="cuda", generator=g) * 0.02).to(dt).contiguous()
+    c = torch.empty(bsz, m, n, device="cuda", dtype=dt)
+    for _ in range(STEPS // 2 + 1):
+        torch.bmm(a, b, out=c)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(STEPS):
+        torch.bmm(a, b, out=c)
+    e1.record()
+    e1.synchronize()
+    out[name] = e0.elapsed_time(e1) / STEPS
+    del a, b, c
+print(json.dumps({"torch": torch.__version__, "ms": out,
+                  "allow_tf32": torch.backends.cuda.matmul.allow_tf32}))
+"""
+
+
+def vendor_gemm(steps):
+    """Time torch.bmm on the config-4 shapes in a child process."""
+    import subprocess
+    code = _VENDOR_GEMM.replace("STEPS", str(max(2, steps)))
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        return {"error": proc.stderr.strip().splitlines()[-1] if proc.stderr.strip() else f"rc {proc.returncode}"}
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    flops = 2.0 * 32 * 2048 * 2048 * 2048
+    r["TFLOP/s"] = {k: flops / (v * 1e-3) / 1e12 for k, v in r["ms"].items()}
+    log("torch.bmm: " + "  ".join(f"{k} {v * 1e3:.1f} us {r['TFLOP/s'][k]:.1f} TF/s" for k, v in r["ms"].items()))
+    return r
+
+
 # ---------------------------------------------------------------- config 5
 def mlp_family(steps, warmup):
     """MLP training step (784->1024->1024->10, batch 4096, softmax-CE,
@@ -450,6 +493,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--only", default="reduce,fused,gemm,mlp,eager")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--vendor", action="store_true",
+                    help="also time torch.bmm on the config-4 shapes (child process; comparison only)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 128 MiB device copy first (reference for PMC byte counters)")
     args = ap.parse_args()
@@ -479,6 +524,8 @@ def main():
         fams["fused"] = fused_family(args.steps, args.warmup)
     if "gemm" in only:
         fams["gemm"] = gemm_family(args.steps, args.warmup)
+        if args.vendor:
+            fams["gemm"]["vendor_torch_bmm"] = vendor_gemm(args.steps)
     # config 5 is reported beside the metric (it is not one of its families)
     extra = {}
     if "mlp" in only:
