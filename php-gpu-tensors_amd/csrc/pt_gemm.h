@@ -109,4 +109,8 @@ int gemm_ring_bk(int variant);
 int gemm_ring_kmul(int variant);
 void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s);
 
+// fp32 products with N <= 16 and k-contiguous A (pt_gemm_smalln.hip).
+bool gemm_smalln_eligible(const GemmArgs &g);
+void launch_gemm_smalln(const GemmArgs &g, hipStream_t s);
+
 }  // namespace pt

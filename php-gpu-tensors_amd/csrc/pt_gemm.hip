@@ -277,13 +277,15 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
             for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
     const int KT = (Kl + BK - 1) / BK;
+    // Loads past the last K step re-read the last one (in bounds, never
+    // stored to LDS as a step's data): with no branch around the loads the
+    // compiler knows exactly which loads are in flight, and waits for the
+    // staged step only, never for the one issued after it.
     // A(m, k): r = m, s_r = a_sm, s_k = a_sk.  B(k, n): r = n, s_r = b_sn, s_k = b_sk.
     la[0].load(A, g.a_sm, g.a_sk, m0, g.M, 0, Kl, tid, g.vec_a);
     lb[0].load(B, g.b_sn, g.b_sk, n0, g.N, 0, Kl, tid, g.vec_b);
-    if (KT > 1) {
-        la[1].load(A, g.a_sm, g.a_sk, m0, g.M, BK, Kl, tid, g.vec_a);
-        lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, BK, Kl, tid, g.vec_b);
-    }
+    la[1].load(A, g.a_sm, g.a_sk, m0, g.M, min(1, KT - 1) * BK, Kl, tid, g.vec_a);
+    lb[1].load(B, g.b_sn, g.b_sk, n0, g.N, min(1, KT - 1) * BK, Kl, tid, g.vec_b);
     la[0].template store<LDA>(lds_a[0], tid);
     lb[0].template store<LDB>(lds_b[0], tid);
     __syncthreads();
@@ -324,10 +326,9 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
     // step kt: W holds tile kt+1 (to LDS after the MFMAs), L receives tile kt+2
     auto step = [&](int kt, LoaderA &wa, LoaderB &wb, LoaderA &la_, LoaderB &lb_) {
         const int cur = kt & 1;
-        if (kt + 2 < KT) {
-            la_.load(A, g.a_sm, g.a_sk, m0, g.M, (kt + 2) * BK, Kl, tid, g.vec_a);
-            lb_.load(B, g.b_sn, g.b_sk, n0, g.N, (kt + 2) * BK, Kl, tid, g.vec_b);
-        }
+        const int kload = min(kt + 2, KT - 1) * BK;
+        la_.load(A, g.a_sm, g.a_sk, m0, g.M, kload, Kl, tid, g.vec_a);
+        lb_.load(B, g.b_sn, g.b_sk, n0, g.N, kload, Kl, tid, g.vec_b);
 #pragma unroll
         for (int sl = 0; sl < NS; sl++) {
             if (sl + 1 < NS)
@@ -348,12 +349,11 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
                 __builtin_amdgcn_sched_group_barrier(0x008, TM * TN, 0);
             }
         }
-        if (kt + 1 < KT) {
-            wa.template store<LDA>(lds_a[cur ^ 1], tid);
-            wb.template store<LDB>(lds_b[cur ^ 1], tid);
-        }
+        // the last step stores and reads a re-read copy that no MFMA uses
+        wa.template store<LDA>(lds_a[cur ^ 1], tid);
+        wb.template store<LDB>(lds_b[cur ^ 1], tid);
         __syncthreads();
-        if (kt + 1 < KT) read_frags(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, fa[0], fb[0]);
+        read_frags(lds_a[cur ^ 1], lds_b[cur ^ 1], 0, fa[0], fb[0]);
     };
     for (int kt = 0; kt < KT; kt += 2) {
         step(kt, la[1], lb[1], la[0], lb[0]);
@@ -453,7 +453,16 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
     float acc = partial[i];
-    for (int k = 1; k < ksplit; k++) acc += partial[(size_t)k * count + i];
+    int k = 1;
+    // sixteen partials in flight per thread; the additions stay in chunk order
+    for (; k + 16 <= ksplit; k += 16) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = partial[(size_t)(k + u) * count + i];
+#pragma unroll
+        for (int u = 0; u < 16; u++) acc += v[u];
+    }
+    for (; k < ksplit; k++) acc += partial[(size_t)k * count + i];
     store_c<DT>(c, i, acc);
 }
 
@@ -878,6 +887,16 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     g.a_sk = (long long)strides_a[nd_a - 1];
     g.b_sk = (long long)strides_b[nd_b - 2];
     g.b_sn = (long long)strides_b[nd_b - 1];
+
+    // fp32 products with at most 16 columns and k-contiguous A stream A
+    // through the small-N kernel (pt_gemm_smalln.hip) unless a tile is forced
+    if (dtype == PT_FLOAT32 && g_tile_override < 0 && batch <= 65535 && gemm_smalln_eligible(g)) {
+        launch_gemm_smalln(g, s);
+        PT_LAUNCH_CHECK("matmul (small-N kernel)");
+        counters().mfma_gemm_calls++;
+        snprintf(counters().last_matmul, sizeof(counters().last_matmul), "mfma-fp32-smalln");
+        return PT_OK;
+    }
 
     const int PKe = dtype == PT_FLOAT32 ? 4 : 8;
     // layout classes: k-contiguous or row/col-contiguous; anything else is

@@ -79,11 +79,14 @@ def _ints(shape, seed, lo=-8, hi=8):
 def test_matmul_integer_exact(A, bmnk, dt, tile):
     b_, m, n, k = bmnk
     A.load().pt_matmul_set_tile(tile)
-    a32 = _ints((b_, m, k), seed=m * 7 + k)
-    b32 = _ints((b_, k, n), seed=n * 5 + k + 1)
-    a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
-    got = run(A, a, b, dt)
-    assert np.array_equal(got, ref(a, b, dt))
+    try:
+        a32 = _ints((b_, m, k), seed=m * 7 + k)
+        b32 = _ints((b_, k, n), seed=n * 5 + k + 1)
+        a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
+        got = run(A, a, b, dt)
+        assert np.array_equal(got, ref(a, b, dt))
+    finally:
+        A.load().pt_matmul_set_tile(-1)
 
 
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
@@ -99,7 +102,11 @@ def test_matmul_split_k(A, bmnk, dt):
     a = O.to_storage(_ints((b_, m, k), seed=k + 3, lo=-3, hi=3), dt)
     b = O.to_storage(_ints((b_, k, n), seed=k + 4, lo=-3, hi=3), dt)
     assert np.array_equal(run(A, a, b, dt), ref(a, b, dt))
-    assert A.backend_info().last_matmul.decode().endswith("splitk")
+    path = A.backend_info().last_matmul.decode()
+    if dt == O.F32 and n <= 16 and m * k >= 1 << 18:
+        assert path == "mfma-fp32-smalln"   # the streaming small-N kernel
+    else:
+        assert path.endswith("splitk")
     a = O.to_storage(synthetic.normal((b_, m, k), 0.0, 1.0, seed=k + 5), dt)
     b = O.to_storage(synthetic.normal((b_, k, n), 0.0, 1.0, seed=k + 6), dt)
     got = O.from_storage(run(A, a, b, dt), dt).astype(np.float64)
@@ -167,6 +174,61 @@ def test_matmul_ring_kernel(A, tile, dt, layout, bmnk):
             b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
             kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
         assert np.array_equal(run(A, a, b_in, dt, **kw), expect)
+    finally:
+        A.load().pt_matmul_set_tile(-1)
+
+
+@pytest.mark.parametrize("layout", ["NN", "TN", "NT"])
+@pytest.mark.parametrize("bmnk", [(1, 4096, 10, 1024), (1, 1024, 10, 4096), (2, 333, 7, 2500),
+                                  (1, 100, 16, 3000), (3, 517, 1, 700), (1, 64, 8, 4096)], ids=str)
+def test_matmul_smalln(A, bmnk, layout):
+    """fp32 products with N <= 16 and k-contiguous A run the small-N kernel
+    (pt_gemm_smalln.hip: eight waves over interleaved 16-k groups, B in LDS
+    chunks of 1024 k rows, so K = 2500, 3000 and 4096 run several chunks);
+    a transposed A (TN) keeps the MFMA tiles.  Integer inputs: bit-exact;
+    random inputs: the fp32 bar of the module docstring.  Ragged M (333,
+    517, 100) and N = 1, 7, 8, 10, 16 cover the column padding and the
+    clamped rows."""
+    from phptensors import synthetic
+    b_, m, n, k = bmnk
+    for trial in ("ints", "normal"):
+        if trial == "ints":
+            a = _ints((b_, m, k), seed=m + k, lo=-3, hi=3)
+            b = _ints((b_, k, n), seed=n + k, lo=-3, hi=3)
+        else:
+            a = synthetic.normal((b_, m, k), 0.0, 1.0, seed=m + k + 1).astype(np.float32)
+            b = synthetic.normal((b_, k, n), 0.0, 1.0, seed=n + k + 1).astype(np.float32)
+        expect = ref(a, b, O.F32)
+        kw = {}
+        a_in, b_in = a, b
+        if layout == "TN":   # A as the transposed view of a [b, k, m] buffer
+            a_in = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+            kw.update(shape_a=(b_, m, k), strides_a=[m * k, 1, m])
+        if layout == "NT":   # B as the transposed view of a [b, n, k] buffer
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+            kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
+        got = run(A, a_in, b_in, O.F32, **kw)
+        path = A.backend_info().last_matmul.decode()
+        if layout == "TN":
+            assert path.startswith("mfma-fp32") and "smalln" not in path
+        else:
+            assert path == "mfma-fp32-smalln"
+        if trial == "ints":
+            assert np.array_equal(got, expect)
+        else:
+            scale = np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))
+            assert np.all(np.abs(got.astype(np.float64) - expect.astype(np.float64)) <= 1e-4 * math.sqrt(k) * scale)
+
+
+def test_matmul_smalln_forced_tile(A):
+    """A forced tile bypasses the small-N kernels (the tile sweeps measure
+    the MFMA kernels on these shapes too)."""
+    A.load().pt_matmul_set_tile(2)
+    try:
+        a = _ints((1, 1024, 512), seed=3)
+        b = _ints((1, 512, 10), seed=4)
+        assert np.array_equal(run(A, a, b, O.F32), ref(a, b, O.F32))
+        assert A.backend_info().last_matmul.decode().startswith("mfma-fp32")
     finally:
         A.load().pt_matmul_set_tile(-1)
 
