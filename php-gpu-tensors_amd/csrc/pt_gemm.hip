@@ -920,10 +920,10 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     const char *suffix = tuned ? "-tuned" : "";
     if (tile < 0) {
         long long t256 = ((g.M + 255) / 256) * (long long)((g.N + 255) / 256) * batch;
-        // mid-size fp32: 128x128 tiles of 8 waves when B is n-contiguous,
-        // 128x64 tiles at two workgroups per CU when B is k-contiguous (the
-        // faster of the two for each layout of the config-5 products)
-        const int mid32 = g.b_sn == 1 ? TILE_128x128_W8 : TILE_128x64_W4M2;
+        // mid-size fp32: 128x128 tiles of 8 waves for either layout of B
+        // (dZ2 W2^T of config 5, B k-contiguous: 76-78 us against 82-84 us
+        // for 128x64 tiles at two workgroups per CU)
+        const int mid32 = TILE_128x128_W8;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
                    ? (dtype == PT_FLOAT32 ? TILE_256x128_W8
                       : dtype == PT_BFLOAT16 ? TILE_RING_DEFAULT : TILE_RING_DEFAULT_F16)
