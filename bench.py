@@ -149,11 +149,26 @@ def reduce_family(steps, warmup):
         log(f"reduce {kind}: {ms * 1e3:.1f} us  {gbs:.0f} GB/s  {100 * gbs / HBM_PEAK_GBS:.1f}% of HBM")
     total_ms = sum(r["ms"] for r in results.values())
     total_bytes = sum(r["bytes"] for r in results.values())
+    # the HIP runtime's device-to-device copy of X (same bytes read and
+    # written as softmax / layerNorm): the practical ceiling of a kernel
+    # that streams one read and one write of equal size on this box
+    def copy(stream, r):
+        A.check(lib.pt_memcpy_d2d(big.ptr, xs[r % replicas].ptr, nbytes, stream), "copy")
+    t = GraphTimer(copy, reps=2 * replicas)
+    t.run(max(1, warmup))
+    ms = t.run(max(1, steps))
+    t.close()
+    copy_gbs = row_bytes / (ms * 1e-3) / 1e9
+    log(f"reduce copy reference (hipMemcpy D2D of X): {ms * 1e3:.1f} us  {copy_gbs:.0f} GB/s  "
+        f"{100 * copy_gbs / HBM_PEAK_GBS:.1f}% of HBM")
     fam = {"workload": "config2: X[8192,4096] fp32 N(0,1) seed 2; sum/mean/max/argmax/var(-1), "
                        "softmax(-1), layerNorm([1],1e-5,1,0)",
            "ms_per_step": total_ms, "GB/s": total_bytes / (total_ms * 1e-3) / 1e9,
            "frac": total_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "ops": results,
-           "replicas": replicas}
+           "replicas": replicas,
+           "copy_reference": {"op": "hipMemcpyAsync device-to-device of X (not timed in value)",
+                              "ms": ms, "bytes": row_bytes, "GB/s": copy_gbs,
+                              "frac": copy_gbs / HBM_PEAK_GBS}}
     return fam
 
 

@@ -126,6 +126,26 @@ __device__ __forceinline__ float fmin_c(float a, float b) { return fminf(a, b); 
 __device__ __forceinline__ double fmin_c(double a, double b) { return fmin(a, b); }
 __device__ __forceinline__ float exp_c(float a) { return expf(a); }
 __device__ __forceinline__ double exp_c(double a) { return exp(a); }
+
+// a / b for many a and one b.  fp32: with rb = RN(1 / b) (one true division
+// per row), q0 = RN(a rb) is within one ulp of a / b and the fma remainder
+// a - b q0 is exact, so RN(q0 + (a - b q0) rb) is the correctly rounded
+// quotient (Markstein's theorem; outside the subnormal range, where it
+// stays within one ulp): three instructions instead of the ~10 of an IEEE
+// division.  Callers take the true division when rb is 0 or not finite.
+struct RowDiv {
+    float b, rb;
+    bool fast;
+    __device__ __forceinline__ explicit RowDiv(float den) : b(den), rb(1.0f / den)
+    {
+        fast = __builtin_isfinite(rb) && rb != 0.0f;
+    }
+    __device__ __forceinline__ float operator()(float a) const
+    {
+        const float q0 = a * rb;
+        return __builtin_fmaf(__builtin_fmaf(-q0, b, a), rb, q0);
+    }
+};
 __device__ __forceinline__ float sqrt_c(float a) { return sqrtf(a); }
 __device__ __forceinline__ double sqrt_c(double a) { return sqrt(a); }
 
@@ -382,11 +402,14 @@ __device__ __forceinline__ int chunk_start(int c, int wr, int lane)
     return ((c * WPR + wr) * 64 + lane) * VEC;
 }
 
+// `full`: every lane's last chunk lies inside the row, judged from lane 63
+// so that it is uniform over the wave and guards whole rows with one scalar
+// branch instead of a lane mask per element.
 template <int DT, int VEC, int NCH, int WPR, bool NT, typename CT>
 __device__ __forceinline__ bool load_row(const typename RT<DT>::S *x, int n, int wr, int lane, CT pad,
                                          CT (&v)[NCH][VEC])
 {
-    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, 63) + VEC <= n;  // wave-uniform
     if (full) {
 #pragma unroll
         for (int c = 0; c < NCH; c++) {
@@ -457,7 +480,7 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
     if (row >= rows) return;  // WPR > 1: one row per block, never taken
     const S *x = (const S *)xin + row * ld;
     C v[NCH][VEC];
-    load_row<DT, VEC, NCH, WPR, true>(x, n, wr, lane, (C)0, v);
+    const bool full = load_row<DT, VEC, NCH, WPR, true>(x, n, wr, lane, (C)0, v);
     C s = 0;
 #pragma unroll
     for (int c = 0; c < NCH; c++)
@@ -465,14 +488,24 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
         for (int k = 0; k < VEC; k++) s = s + v[c][k];
     const C mean = row_sum<C, WPR>(s, lds) / (C)n;
     C q = 0;
+    // v - v keeps infinities poisoning the result as in Welford
+    if (full) {  // wave-uniform: no per-element guard on whole rows
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        const int i = chunk_start<VEC, WPR>(c, wr, lane);
+        for (int c = 0; c < NCH; c++)
 #pragma unroll
-        for (int k = 0; k < VEC; k++) {
-            // v - v keeps infinities poisoning the result as in Welford
-            C d = i + k < n ? v[c][k] - mean + (v[c][k] - v[c][k]) : (C)0;
-            q = q + d * d;
+            for (int k = 0; k < VEC; k++) {
+                const C d = v[c][k] - mean + (v[c][k] - v[c][k]);
+                q = q + d * d;
+            }
+    } else {
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                const C d = i + k < n ? v[c][k] - mean + (v[c][k] - v[c][k]) : (C)0;
+                q = q + d * d;
+            }
         }
     }
     q = row_sum<C, WPR>(q, lds);
@@ -499,7 +532,7 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
     size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
     const size_t row_step = RW ? (size_t)gridDim.x * (4 / WPR) : rows;
     if (row >= rows) return;  // WPR > 1: uniform per block
-    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, 63) + VEC <= n;  // wave-uniform
     C nx[NCH][VEC];
     if constexpr (RW) load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * ld, n, wr, lane, neg_inf<C>(), nx);
     for (; row < rows; row += row_step) {
@@ -523,21 +556,47 @@ __global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xi
             for (int k = 0; k < VEC; k++) m = fmax_c(m, v[c][k]);
         m = row_max<C, WPR>(m, lds);
         C sum = 0;
+        if (full) {  // wave-uniform: no per-element guard on whole rows
 #pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+            for (int c = 0; c < NCH; c++)
 #pragma unroll
-            for (int k = 0; k < VEC; k++) {
-                C e = (full || i + k < n) ? exp_c(v[c][k] - m) : (C)0;
-                v[c][k] = e;
-                sum = sum + e;
+                for (int k = 0; k < VEC; k++) {
+                    const C e = exp_c(v[c][k] - m);
+                    v[c][k] = e;
+                    sum = sum + e;
+                }
+        } else {
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+                for (int k = 0; k < VEC; k++) {
+                    const C e = i + k < n ? exp_c(v[c][k] - m) : (C)0;
+                    v[c][k] = e;
+                    sum = sum + e;
+                }
             }
         }
         sum = row_sum<C, WPR>(sum, lds);
+        if constexpr (sizeof(C) == 4) {
+            const RowDiv div(sum);
+            if (div.fast) {
 #pragma unroll
-        for (int c = 0; c < NCH; c++)
+                for (int c = 0; c < NCH; c++)
 #pragma unroll
-            for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
+                    for (int k = 0; k < VEC; k++) v[c][k] = div(v[c][k]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < NCH; c++)
+#pragma unroll
+                    for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < NCH; c++)
+#pragma unroll
+                for (int k = 0; k < VEC; k++) v[c][k] = v[c][k] / sum;
+        }
         store_row<VEC, NCH, WPR, SNT>(y, n, wr, lane, full, v);
     }
 }
@@ -574,7 +633,7 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
     size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
     const size_t row_step = WPR > 1 ? (size_t)gridDim.x : rows;
     if (row >= rows) return;  // WPR > 1: uniform per block
-    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, lane) + VEC <= n;
+    const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, 63) + VEC <= n;  // wave-uniform
     CT g[NCH][VEC], b[NCH][VEC];
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
@@ -616,27 +675,47 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
             for (int k = 0; k < VEC; k++) s = s + v[c][k];
         const CT mean = row_sum<CT, WPR>(s, lds) / (CT)n;
         CT q = 0;
+        if (full) {  // wave-uniform: no per-element guard on whole rows
 #pragma unroll
-        for (int c = 0; c < NCH; c++) {
-            const int i = chunk_start<VEC, WPR>(c, wr, lane);
+            for (int c = 0; c < NCH; c++)
 #pragma unroll
-            for (int k = 0; k < VEC; k++) {
-                CT d = (full || i + k < n) ? v[c][k] - mean : (CT)0;
-                v[c][k] = d;
-                q = q + d * d;
+                for (int k = 0; k < VEC; k++) {
+                    const CT d = v[c][k] - mean;
+                    v[c][k] = d;
+                    q = q + d * d;
+                }
+        } else {
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+                const int i = chunk_start<VEC, WPR>(c, wr, lane);
+#pragma unroll
+                for (int k = 0; k < VEC; k++) {
+                    const CT d = i + k < n ? v[c][k] - mean : (CT)0;
+                    v[c][k] = d;
+                    q = q + d * d;
+                }
             }
         }
         q = row_sum<CT, WPR>(q, lds);
         const CT dev = sqrt_c(q / (CT)n + eps);
+        auto finish = [&](auto quot) {
 #pragma unroll
-        for (int c = 0; c < NCH; c++) {
+            for (int c = 0; c < NCH; c++) {
 #pragma unroll
-            for (int k = 0; k < VEC; k++) {
-                CT t = v[c][k] / dev;
-                if (gamma) t = t * g[c][k];
-                if (beta) t = t + b[c][k];
-                v[c][k] = t;
+                for (int k = 0; k < VEC; k++) {
+                    CT t = quot(v[c][k]);
+                    if (gamma) t = t * g[c][k];
+                    if (beta) t = t + b[c][k];
+                    v[c][k] = t;
+                }
             }
+        };
+        if constexpr (sizeof(CT) == 4) {
+            const RowDiv div(dev);
+            if (div.fast) finish(div);
+            else finish([&](CT a) { return a / dev; });
+        } else {
+            finish([&](CT a) { return a / dev; });
         }
         store_row<VEC, NCH, WPR, SNT>(y, n, wr, lane, full, v);
     }
