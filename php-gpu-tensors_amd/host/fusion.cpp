@@ -1383,6 +1383,21 @@ static bool run_steps(Plan &p, std::vector<TensorP> &vals)
 // values and the order of every dependency are unchanged.
 static constexpr int kBranches = 3;
 
+// The side streams of the branches (this thread's), created outside any
+// graph capture.
+static bool branch_streams(std::vector<pt_stream_t> &streams)
+{
+    static thread_local std::vector<pt_stream_t> side;
+    while ((int)side.size() < kBranches - 1) {
+        pt_stream_t s = nullptr;
+        if (!check_status(pt_stream_create(&s), "Fusion branch stream")) return false;
+        side.push_back(s);
+    }
+    streams = {pt_default_stream()};
+    for (pt_stream_t s : side) streams.push_back(s);
+    return true;
+}
+
 static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<pt_event_t> &events)
 {
     const int ns = (int)p.steps.size();
@@ -1399,14 +1414,8 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
             id = p.items[id].args[0];
         return id;
     };
-    static thread_local std::vector<pt_stream_t> side;
-    while ((int)side.size() < kBranches - 1) {
-        pt_stream_t s = nullptr;
-        if (!check_status(pt_stream_create(&s), "Fusion branch stream")) return false;
-        side.push_back(s);
-    }
-    std::vector<pt_stream_t> streams = {pt_default_stream()};
-    for (pt_stream_t s : side) streams.push_back(s);
+    std::vector<pt_stream_t> streams;
+    if (!branch_streams(streams)) return false;
     auto new_event = [&](pt_event_t &e) {
         if (!check_status(pt_event_create(&e), "Fusion branch event")) return false;
         events.push_back(e);
@@ -1531,6 +1540,10 @@ static bool measuring_run(Plan &p, std::vector<TensorP> &vals)
 static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, bool &captured)
 {
     captured = false;
+    std::vector<pt_stream_t> streams;
+    if (!branch_streams(streams)) return false;  // before the capture begins
+    const uint64_t refusals = allocation_refusals();
+    reset_failed_status();
     if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
     bool ok = true;
     // branch events stay alive until the capture has ended
@@ -1554,6 +1567,11 @@ static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, boo
         pt_stream_set_current(nullptr);
         pt_graph_t scrap = nullptr;
         if (pt_graph_end_capture(nullptr, &scrap) == PT_OK && scrap) pt_graph_destroy(scrap);
+        // only a refused allocation (a native that needs a temporary, or
+        // scratch beyond the measured workspace) makes the plan eager; any
+        // other failure is the caller's error, with its own message
+        const bool allocation = allocation_refusals() != refusals || last_failed_status() == PT_ERR_NOMEM;
+        if (!allocation) return false;
         p.graph_compatible = false;
         p.incompatibility = "a native step allocates during capture";
         clear_error();
@@ -2025,7 +2043,8 @@ const char *phpt_graph_stats(phpt_graph *g)
        << ";graphLaunches=" << p.graph_launches << ";bufferReuses=" << p.buffer_reuses
        << ";pending=" << p.pending << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)
        << ";tensorAllocations=" << p.tensor_allocations << ";synchronizations=" << p.synchronizations
-       << ";workspaceBuffers=" << p.cache.size() + (p.workspace ? 1 : 0) << ";profiling=" << (p.profiling ? 1 : 0)
+       << ";workspaceBuffers=" << p.cache.size() + (p.workspace ? 1 : 0)
+       << ";workspaceBytes=" << (p.workspace ? p.workspace_bytes : 0) << ";profiling=" << (p.profiling ? 1 : 0)
        << ";profiledExecutions=" << p.profiled << ";bindTimeNs=" << p.bind_ns
        << ";executeTimeNs=" << p.execute_ns << ";collectTimeNs=" << p.collect_ns << ";";
     t_text = os.str();

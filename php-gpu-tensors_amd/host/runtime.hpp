@@ -28,6 +28,8 @@ void clear_error();
 int error_kind();
 const char *error_message();
 bool check_status(pt_status st, const char *what);  // false + error set on failure
+pt_status last_failed_status();  // status of the latest check_status that failed
+void reset_failed_status();
 
 // ------------------------------------------------------------------ dtypes
 // dtype_t numbering of src/data_types.h:8-25 (PT_* codes).
@@ -112,6 +114,7 @@ TensorP materialize(const TensorP &t);                       // contiguous copy 
 // step its (stable) output buffer with preset_output; the native operation
 // takes it through output_tensor when shape and dtype match.
 bool &allocation_forbidden();
+uint64_t allocation_refusals();  // allocations refused while forbidden (this thread)
 void preset_output(const TensorP &t);
 TensorP output_tensor(const int *shape, int ndims, int dtype);
 

@@ -51,9 +51,14 @@ void clear_error()
 int error_kind() { return t_kind; }
 const char *error_message() { return t_msg; }
 
+static thread_local pt_status t_last_status = PT_OK;
+pt_status last_failed_status() { return t_last_status; }
+void reset_failed_status() { t_last_status = PT_OK; }
+
 bool check_status(pt_status st, const char *what)
 {
     if (st == PT_OK) return true;
+    t_last_status = st;
     const char *detail = pt_last_error();
     if (st == PT_ERR_INVALID) set_invalid("%s", detail && *detail ? detail : what);
     else set_runtime("%s: %s", what, detail ? detail : pt_status_string(st));
@@ -452,9 +457,11 @@ TensorP make_meta(const int *shape, int ndims, int dtype)
 }
 
 static thread_local bool t_alloc_forbidden = false;
+static thread_local uint64_t t_alloc_refusals = 0;
 static thread_local TensorP t_preset;
 
 bool &allocation_forbidden() { return t_alloc_forbidden; }
+uint64_t allocation_refusals() { return t_alloc_refusals; }
 
 void preset_output(const TensorP &t) { t_preset = t; }
 
@@ -471,6 +478,7 @@ TensorP output_tensor(const int *shape, int ndims, int dtype)
 TensorP make_empty(const int *shape, int ndims, int dtype)
 {
     if (t_alloc_forbidden) {
+        t_alloc_refusals++;
         set_runtime("Device allocation inside a captured plan");
         return nullptr;
     }
