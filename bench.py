@@ -430,31 +430,33 @@ def mlp_family(steps, warmup):
 
 
 def mlp_cpu_baseline(sample_rows=256):
-    """float64 numpy restatement of the step on a row sample, BLAS on one thread."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import mlp_ref as R
-    from phptensors import mlp
-    try:
-        from threadpoolctl import threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_limits = None
-    layers = (784, 1024, 1024, 10)
-    params = [p.toNumpy().astype(np.float64) for p in mlp.init_parameters(layers, 5)]
-    x, y = mlp.synthetic_batch(sample_rows, layers[0], layers[-1], 5)
-    zeros = [np.zeros_like(p) for p in params]
-    ctx = threadpool_limits(limits=1) if threadpool_limits else None
-    try:
-        if ctx:
-            ctx.__enter__()
-        t0 = time.perf_counter()
-        R.train_step(x, y, params, zeros, zeros, 1.0, 1.0, 1e-3, mlp.DECAY_MASK)
-        dt = time.perf_counter() - t0
-    finally:
-        if ctx:
-            ctx.__exit__(None, None, None)
-    flops = mlp.step_flops(sample_rows, layers)
+    """The reference's CPU path for the config-5 step: its eight GEMMs at the
+    config-5 shapes through the oracle's HostArray matmul restatement
+    (sequential fmaf, contiguous_array_ce.c:1295-1343), one core, on a row
+    sample.  Every product of the step is linear in the batch rows (M for
+    the forward and input-gradient products, K for the weight gradients), so
+    the sample's rate is the full step's; the elementwise, loss and AdamW
+    work (under 0.1 % of the step's FLOPs) is left out."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle_lib as O
+    r = sample_rows
+    # (M, K, N): forward x.W1, h1.W2, h2.W3; backward dZ3.W3^T, dZ2.W2^T,
+    # h2^T.dZ3, h1^T.dZ2, x^T.dZ1
+    shapes = [(r, 784, 1024), (r, 1024, 1024), (r, 1024, 10), (r, 10, 1024), (r, 1024, 1024),
+              (1024, r, 10), (1024, r, 1024), (784, r, 1024)]
+    ops = []
+    for i, (m, k, n) in enumerate(shapes):
+        ops.append((synthetic.normal((m, k), 0.0, 0.05, seed=50 + i),
+                    synthetic.normal((k, n), 0.0, 0.05, seed=70 + i)))
+    t0 = time.perf_counter()
+    for a, b in ops:
+        O.matmul(a, b, O.F32)
+    dt = time.perf_counter() - t0
+    flops = sum(2.0 * m * k * n for m, k, n in shapes)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"{sample_rows} of 4096 rows, float64 numpy step on one BLAS thread; {dt:.2f} s"}
+            "step_ms_at_4096_rows": dt * 4096 / r * 1e3,
+            "sample": f"the step's 8 GEMMs at {r} of 4096 rows through the oracle's HostArray matmul "
+                      f"restatement (sequential fmaf) on one host core; {dt:.2f} s"}
 
 
 def _to_bf16(x):
