@@ -429,6 +429,36 @@ def mlp_family(steps, warmup):
             "plan_kernels": kinds.count("fused"), "workspace_bytes": graph.getStats().get("workspaceBytes")}
 
 
+def transfer_family(steps, nbytes=256 << 20):
+    """Host <-> device transfers through pt_memcpy_h2d / pt_memcpy_d2h
+    (tensor_transfer.c:45-65): a pageable numpy buffer (staged through the
+    library's pinned ring) and a pinned one (pt_host_alloc_pinned, copied
+    directly: the link's own rate), each timed on the host clock around the
+    synchronous call, best of `steps`."""
+    lib = A.load()
+    dev = A.DeviceBuffer(nbytes)
+    pageable = np.full(nbytes, 7, np.uint8)
+    pinned = ctypes.c_void_p()
+    A.check(lib.pt_host_alloc_pinned(ctypes.byref(pinned), nbytes), "pinned")
+    out = {"bytes": nbytes}
+    try:
+        np.ctypeslib.as_array((ctypes.c_uint8 * nbytes).from_address(pinned.value))[:] = 7
+        for name, host in (("pageable", pageable.ctypes.data), ("pinned", pinned.value)):
+            for way, fn in (("h2d", lambda: lib.pt_memcpy_h2d(dev.ptr, host, nbytes, None)),
+                            ("d2h", lambda: lib.pt_memcpy_d2h(host, dev.ptr, nbytes, None))):
+                best = None
+                for _ in range(max(3, steps)):
+                    t0 = time.perf_counter()
+                    A.check(fn(), way)
+                    dt = time.perf_counter() - t0
+                    best = dt if best is None else min(best, dt)
+                out[f"{way}_{name}_GB/s"] = round(nbytes / best / 1e9, 1)
+    finally:
+        A.check(lib.pt_host_free_pinned(pinned.value), "free pinned")
+    log(f"transfers: {out}")
+    return out
+
+
 def mlp_cpu_baseline(sample_rows=256):
     """The reference's CPU path for the config-5 step: its eight GEMMs at the
     config-5 shapes through the oracle's HostArray matmul restatement
@@ -508,7 +538,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--only", default="reduce,fused,gemm,mlp,eager")
+    ap.add_argument("--only", default="reduce,fused,gemm,mlp,eager,transfer")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--vendor", action="store_true",
                     help="also time torch.bmm on the config-4 shapes (child process; comparison only)")
@@ -549,6 +579,8 @@ def main():
         extra["mlp"] = mlp_family(max(1, args.steps // 2), args.warmup)
     if "eager" in only:
         extra["eager"] = eager_family(args.steps, args.warmup)
+    if "transfer" in only:
+        extra["transfer"] = transfer_family(args.steps)
     wall = time.perf_counter() - t_wall
 
     # dominant kernel: the largest share of a step (time per launch x
@@ -619,6 +651,7 @@ def main():
         "kernels": kernels,
         "config5_mlp": extra.get("mlp"),
         "config3_eager": extra.get("eager"),
+        "transfers": extra.get("transfer"),
         "cpu_baseline": cpu,
         "wall_s": round(wall, 2),
     }

@@ -150,7 +150,10 @@ pt_status pt_alloc(void **ptr, size_t bytes, pt_stream_t stream);
 pt_status pt_free(void *ptr, pt_stream_t stream);
 pt_status pt_mem_info(size_t *free_bytes, size_t *total_bytes, size_t *pool_reserved);
 /* Transfers (replace cudaMemcpy in src/cuda_array/tensor_transfer.c:45-65,
- * src/cuda_array/tensor_factory.c:301-326).  Synchronous w.r.t. the host. */
+ * src/cuda_array/tensor_factory.c:301-326).  Synchronous w.r.t. the host.
+ * A pageable host buffer of 4 MiB or more is moved through the library's
+ * two pinned 16 MiB chunks, the host copy of one overlapping the DMA of the
+ * other; pinned buffers (pt_host_alloc_pinned) are copied directly. */
 pt_status pt_memcpy_h2d(void *dst, const void *src, size_t bytes, pt_stream_t stream);
 pt_status pt_memcpy_d2h(void *dst, const void *src, size_t bytes, pt_stream_t stream);
 pt_status pt_memcpy_d2d(void *dst, const void *src, size_t bytes, pt_stream_t stream);
@@ -300,6 +303,7 @@ typedef struct {
     uint64_t elementwise_calls;
     uint64_t rtc_compiles;
     uint64_t graph_launches;
+    uint64_t staged_copies;  /* transfers staged through the pinned ring */
 } pt_backend_info;
 pt_status pt_backend_info_get(pt_backend_info *info);
 pt_status pt_backend_info_reset(void);

@@ -420,23 +420,7 @@ pt_status pt_mem_info(size_t *free_bytes, size_t *total_bytes, size_t *pool_rese
     return PT_OK;
 }
 
-pt_status pt_memcpy_h2d(void *dst, const void *src, size_t bytes, pt_stream_t stream)
-{
-    PT_TRY(ensure_init());
-    if (!bytes) return PT_OK;
-    hipStream_t s = stream_of(stream);
-    PT_TRY(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s), "host to device copy"));
-    return check_hip(hipStreamSynchronize(s), "host to device copy");
-}
-
-pt_status pt_memcpy_d2h(void *dst, const void *src, size_t bytes, pt_stream_t stream)
-{
-    PT_TRY(ensure_init());
-    if (!bytes) return PT_OK;
-    hipStream_t s = stream_of(stream);
-    PT_TRY(check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "device to host copy"));
-    return check_hip(hipStreamSynchronize(s), "device to host copy");
-}
+// pt_memcpy_h2d / pt_memcpy_d2h: pt_transfer.hip
 
 pt_status pt_memcpy_d2d(void *dst, const void *src, size_t bytes, pt_stream_t stream)
 {

@@ -61,7 +61,8 @@ class PtBackendInfo(ctypes.Structure):
         (name, ctypes.c_uint64) for name in (
             "mfma_gemm_calls", "generic_gemm_calls", "row_reduce_calls",
             "column_reduce_calls", "strided_reduce_calls", "global_reduce_calls",
-            "fused_row_calls", "elementwise_calls", "rtc_compiles", "graph_launches")]
+            "fused_row_calls", "elementwise_calls", "rtc_compiles", "graph_launches",
+            "staged_copies")]
 
 
 # name -> (restype, argtypes); every function declared in include/pt_hip.h
