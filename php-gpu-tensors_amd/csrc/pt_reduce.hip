@@ -488,13 +488,15 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
         for (int k = 0; k < VEC; k++) s = s + v[c][k];
     const C mean = row_sum<C, WPR>(s, lds) / (C)n;
     C q = 0;
-    // v - v keeps infinities poisoning the result as in Welford
+    // Infinities poison the result as in Welford without a per-element term:
+    // an infinite element makes the row's mean infinite or NaN, and its own
+    // deviation inf - inf is then NaN (a NaN element makes the mean NaN).
     if (full) {  // wave-uniform: no per-element guard on whole rows
 #pragma unroll
         for (int c = 0; c < NCH; c++)
 #pragma unroll
             for (int k = 0; k < VEC; k++) {
-                const C d = v[c][k] - mean + (v[c][k] - v[c][k]);
+                const C d = v[c][k] - mean;
                 q = q + d * d;
             }
     } else {
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
             const int i = chunk_start<VEC, WPR>(c, wr, lane);
 #pragma unroll
             for (int k = 0; k < VEC; k++) {
-                const C d = i + k < n ? v[c][k] - mean + (v[c][k] - v[c][k]) : (C)0;
+                const C d = i + k < n ? v[c][k] - mean : (C)0;
                 q = q + d * d;
             }
         }

@@ -829,15 +829,22 @@ static pt_module_t load_module(const std::string &src, bool &hit)
 }
 
 // ------------------------------------------------------ output regions
-// Dependent-output regions (the reference's fusion_output_regions,
-// fusion_plan.c:250-397, restated): starting from the last output, a region
-// takes every same-shape floating elementwise ancestor of the output (the
-// sum of their operation costs within FUSION_OUTPUT_REGION_BUDGET), then
-// every other output connected to those members, as long as at most four
-// values leave the region (its outputs and members read from outside) and
-// nothing outside it both reads a member and feeds one.  A region of two or
-// more outputs is evaluated by one kernel: its members are not materialized,
-// except those that leave it.
+// Dependent-output regions (the rule of the reference's
+// fusion_output_regions, fusion_plan.c:250-397).  An output is grown into a
+// region of same-shape floating elementwise items: the region takes the
+// output's compatible ancestors, then, output by output in item order and
+// until nothing changes, every other output that reaches the region through
+// compatible items, together with that output's compatible ancestors, while
+// the members' operation costs sum to at most kRegionBudget and at most four
+// outputs are members.  The region stands when it holds two or more outputs,
+// at most four values leave it (member outputs, and members read by other
+// items), and no path leaves it and comes back (a member reading an outside
+// item that depends on a member).  One kernel then evaluates the region;
+// only the values that leave it are materialized.
+//
+// Items are stored after their arguments, so each reachability question is
+// one sweep over the item order: backward for a set of ancestors, forward for
+// "reaches the region".
 static constexpr int kRegionBudget = 128;
 
 static bool region_member_kind(const Plan &p, int id, int shape_of)
@@ -853,6 +860,7 @@ static bool region_member_kind(const Plan &p, int id, int shape_of)
     return t.ndims == r.ndims && std::equal(t.shape, t.shape + t.ndims, r.shape);
 }
 
+// operation cost of one member (the reference's region cost table)
 static int region_op_cost(const Item &it)
 {
     const FusionNode &n = *it.t->node;
@@ -860,40 +868,60 @@ static int region_op_cost(const Item &it)
     return it.t->dtype == PT_FLOAT64 ? 2 * c : c;
 }
 
-// adds `id` and its compatible ancestors; false when the budget is exceeded
-static bool region_collect(const Plan &p, int id, int shape_of, std::vector<char> &members, int &cost)
-{
-    if (members[id]) return true;
-    if (!region_member_kind(p, id, shape_of)) return true;
-    members[id] = 1;
-    cost += region_op_cost(p.items[id]);
-    if (cost > kRegionBudget) return false;
-    for (int a : p.items[id].args)
-        if (!region_collect(p, a, shape_of, members, cost)) return false;
-    return true;
-}
+class RegionBuilder {
+public:
+    RegionBuilder(const Plan &plan, int root) : p_(plan), n_((int)plan.items.size()), compat_(n_, 0)
+    {
+        for (int i = 0; i < n_; i++) compat_[i] = region_member_kind(p_, i, root);
+    }
 
-// true when `id` reaches a member through compatible nodes
-static bool region_connected(const Plan &p, int id, int shape_of, const std::vector<char> &members,
-                             std::vector<char> &seen)
-{
-    if (members[id]) return true;
-    if (seen[id] || !region_member_kind(p, id, shape_of)) return false;
-    seen[id] = 1;
-    for (int a : p.items[id].args)
-        if (region_connected(p, a, shape_of, members, seen)) return true;
-    return false;
-}
+    // Adds `start` and its compatible ancestors that `set` lacks (an item in
+    // `set`, or one that cannot join, is not looked through); false when the
+    // cost then exceeds the budget.
+    bool absorb(int start, std::vector<char> &set, int &cost) const
+    {
+        std::vector<char> wanted(n_, 0);
+        wanted[start] = 1;
+        for (int x = start; x >= 0; x--) {
+            if (!wanted[x] || set[x] || !compat_[x]) continue;
+            set[x] = 1;
+            cost += region_op_cost(p_.items[x]);
+            for (int a : p_.items[x].args) wanted[a] = 1;
+        }
+        return cost <= kRegionBudget;
+    }
 
-// true when `id` reaches a member through any nodes
-static bool region_reenters(const Plan &p, int id, const std::vector<char> &members, std::vector<char> &seen)
+    // r[x]: x is in `set` or one of its arguments reaches it; with
+    // `through_compatible`, only items that can join pass the reach on
+    std::vector<char> reaching(const std::vector<char> &set, bool through_compatible) const
+    {
+        std::vector<char> r(n_, 0);
+        for (int x = 0; x < n_; x++) {
+            if (set[x]) {
+                r[x] = 1;
+                continue;
+            }
+            if (through_compatible && !compat_[x]) continue;
+            for (int a : p_.items[x].args)
+                if (r[a]) {
+                    r[x] = 1;
+                    break;
+                }
+        }
+        return r;
+    }
+
+private:
+    const Plan &p_;
+    const int n_;
+    std::vector<char> compat_;
+};
+
+static int count_outputs(const Plan &p, const std::vector<char> &set)
 {
-    if (members[id]) return true;
-    if (seen[id]) return false;
-    seen[id] = 1;
-    for (int a : p.items[id].args)
-        if (region_reenters(p, a, members, seen)) return true;
-    return false;
+    int k = 0;
+    for (size_t i = 0; i < set.size(); i++) k += set[i] && p.items[i].output;
+    return k;
 }
 
 static void output_regions(Plan &p)
@@ -904,53 +932,46 @@ static void output_regions(Plan &p)
         if (!ri.output || ri.region >= 0 || ri.kind != IT_ELEM ||
             (ri.t->dtype != PT_FLOAT32 && ri.t->dtype != PT_FLOAT64))
             continue;
-        std::vector<char> members(n, 0);
+        const RegionBuilder rb(p, root);
+        std::vector<char> region(n, 0);
         int cost = 0;
-        if (!region_collect(p, root, root, members, cost) || !members[root]) continue;
-        for (bool grew = true; grew;) {
-            grew = false;
-            for (int i = 0; i < n; i++) {
-                if (!p.items[i].output || members[i]) continue;
-                std::vector<char> seen(n, 0);
-                if (!region_connected(p, i, root, members, seen)) continue;
-                std::vector<char> trial = members;
-                int trial_cost = cost;
-                if (!region_collect(p, i, root, trial, trial_cost)) continue;
-                int returned = 0;
-                for (int j = 0; j < n; j++) returned += trial[j] && p.items[j].output;
-                if (returned > 4) continue;
-                members.swap(trial);
-                cost = trial_cost;
-                grew = true;
+        if (!rb.absorb(root, region, cost) || !region[root]) continue;
+        // grow: sweeps over the outputs in item order until one adds nothing
+        bool changed = true;
+        while (changed) {
+            changed = false;
+            for (int o = 0; o < n; o++) {
+                if (!p.items[o].output || region[o]) continue;
+                if (!rb.reaching(region, true)[o]) continue;
+                std::vector<char> grown = region;
+                int grown_cost = cost;
+                if (!rb.absorb(o, grown, grown_cost) || count_outputs(p, grown) > 4) continue;
+                region.swap(grown);
+                cost = grown_cost;
+                changed = true;
             }
         }
-        std::vector<char> leaves_region(n, 0), seen(n, 0);
-        int returned = 0;
-        bool compatible = true;
-        for (int i = 0; i < n && compatible; i++) {
-            if (members[i] && p.items[i].output) {
-                leaves_region[i] = 1;
-                returned++;
-            }
-            for (int c : p.items[i].args) {
-                if (!members[i] && members[c]) leaves_region[c] = 1;
-                if (members[i] && !members[c] && region_reenters(p, c, members, seen)) compatible = false;
+        // validate: values that leave, and no way out and back in
+        const std::vector<char> back = rb.reaching(region, false);
+        std::vector<char> leaves(n, 0);
+        bool closed = true;
+        for (int x = 0; x < n; x++) {
+            if (region[x] && p.items[x].output) leaves[x] = 1;
+            for (int a : p.items[x].args) {
+                if (!region[x] && region[a]) leaves[a] = 1;
+                if (region[x] && !region[a] && back[a]) closed = false;
             }
         }
         int leaving = 0;
-        for (int i = 0; i < n; i++) leaving += leaves_region[i];
-        if (!compatible || returned < 2 || leaving > 4) continue;
-        for (int i = 0; i < n; i++)
-            if (members[i]) {
-                Item &m = p.items[i];
-                m.region = root;
-                if (leaves_region[i]) {
-                    m.cut = true;
-                    if (!m.output) m.reason = "dependent-outputs";
-                } else {
-                    m.cut = false;
-                }
-            }
+        for (int x = 0; x < n; x++) leaving += leaves[x];
+        if (!closed || count_outputs(p, region) < 2 || leaving > 4) continue;
+        for (int x = 0; x < n; x++) {
+            if (!region[x]) continue;
+            Item &m = p.items[x];
+            m.region = root;
+            m.cut = leaves[x] != 0;
+            if (m.cut && !m.output) m.reason = "dependent-outputs";
+        }
     }
 }
 
