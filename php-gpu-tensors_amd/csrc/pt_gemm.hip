@@ -1132,8 +1132,8 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
         n++;
     }
     g_tile_override = saved;
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);  // cleanup: the timing status is what counts
+    (void)hipEventDestroy(e1);
     PT_TRY(st);
     *count = n < max_candidates ? n : max_candidates;
     *selected = best;

@@ -80,7 +80,10 @@ static void init_once()
     // Keep freed blocks cached in the pool (the reference's pool never returns
     // memory to the driver either, memory_pool.c:350-381).
     uint64_t threshold = UINT64_MAX;
-    hipMemPoolSetAttribute(g_pool, hipMemPoolAttrReleaseThreshold, &threshold);
+    if (hipMemPoolSetAttribute(g_pool, hipMemPoolAttrReleaseThreshold, &threshold) != hipSuccess) {
+        g_init_status = fail(PT_ERR_RUNTIME, "could not set the memory pool's release threshold");
+        return;
+    }
     snprintf(g_info.last_matmul, sizeof(g_info.last_matmul), "none");
 }
 
@@ -414,7 +417,8 @@ pt_status pt_mem_info(size_t *free_bytes, size_t *total_bytes, size_t *pool_rese
     if (total_bytes) *total_bytes = t;
     if (pool_reserved) {
         uint64_t reserved = 0;
-        hipMemPoolGetAttribute(g_pool, hipMemPoolAttrReservedMemCurrent, &reserved);
+        PT_TRY(check_hip(hipMemPoolGetAttribute(g_pool, hipMemPoolAttrReservedMemCurrent, &reserved),
+                         "hipMemPoolGetAttribute"));
         *pool_reserved = (size_t)reserved;
     }
     return PT_OK;
@@ -589,7 +593,7 @@ pt_status pt_graph_end_capture(pt_stream_t stream, pt_graph_t *graph)
     h->graph = g;
     hipError_t err = hipGraphInstantiate(&h->exec, g, nullptr, nullptr, 0);
     if (err != hipSuccess) {
-        hipGraphDestroy(g);
+        (void)hipGraphDestroy(g);
         delete h;
         return check_hip(err, "hipGraphInstantiate");
     }
@@ -610,13 +614,13 @@ pt_status pt_graph_end_capture_update(pt_stream_t stream, pt_graph_t graph)
         hipGraphExec_t fresh;
         hipError_t e2 = hipGraphInstantiate(&fresh, g, nullptr, nullptr, 0);
         if (e2 != hipSuccess) {
-            hipGraphDestroy(g);
+            (void)hipGraphDestroy(g);
             return check_hip(e2, "hipGraphInstantiate");
         }
-        hipGraphExecDestroy(h->exec);
+        (void)hipGraphExecDestroy(h->exec);
         h->exec = fresh;
     }
-    if (h->graph) hipGraphDestroy(h->graph);
+    if (h->graph) (void)hipGraphDestroy(h->graph);
     h->graph = g;
     return PT_OK;
 }
@@ -632,8 +636,8 @@ pt_status pt_graph_destroy(pt_graph_t graph)
 {
     GraphHandle *h = (GraphHandle *)graph;
     if (!h) return PT_OK;
-    if (h->exec) hipGraphExecDestroy(h->exec);
-    if (h->graph) hipGraphDestroy(h->graph);
+    if (h->exec) (void)hipGraphExecDestroy(h->exec);
+    if (h->graph) (void)hipGraphDestroy(h->graph);
     delete h;
     return PT_OK;
 }
