@@ -429,6 +429,87 @@ def mlp_family(steps, warmup):
             "plan_kernels": kinds.count("fused"), "workspace_bytes": graph.getStats().get("workspaceBytes")}
 
 
+# The step's products with the operand layouts the compiled plan hands to
+# pt_matmul: name -> (A shape, A strides, B shape, B strides), row-major
+# storage of x [4096, 784], h1 / dZ2 / dZ1 [4096, 1024], W1 [784, 1024],
+# W2 [1024, 1024] (transposes are strided views, as in the plan).
+_MLP_GEMMS = {
+    "G1 x.W1": ((4096, 784), (784, 1), (784, 1024), (1024, 1)),
+    "G2 h1.W2": ((4096, 1024), (1024, 1), (1024, 1024), (1024, 1)),
+    "dH1 dZ2.W2T": ((4096, 1024), (1024, 1), (1024, 1024), (1, 1024)),
+    "dW2 h1T.dZ2": ((1024, 4096), (1, 1024), (4096, 1024), (1024, 1)),
+    "dW1 xT.dZ1": ((784, 4096), (1, 784), (4096, 1024), (1024, 1)),
+}
+
+
+def mlp_gemms(steps):
+    """The five large fp32 products of the config-5 step, each timed alone
+    (graph replays of pt_matmul on synthetic operands of the step's shapes
+    and layouts)."""
+    lib = A.load()
+    rng = np.random.default_rng(5)
+    out = {}
+    c = A.DeviceBuffer(4096 * 1024 * 4)
+    for name, (ash, ast, bsh, bst) in _MLP_GEMMS.items():
+        span_a = 1 + sum((d - 1) * st for d, st in zip(ash, ast))
+        span_b = 1 + sum((d - 1) * st for d, st in zip(bsh, bst))
+        da = A.to_device((rng.standard_normal(span_a, dtype=np.float32) * 0.05).astype(np.float32))
+        db = A.to_device((rng.standard_normal(span_b, dtype=np.float32) * 0.05).astype(np.float32))
+        m, k, n = ash[0], ash[1], bsh[1]
+        sa, sta, sb, stb, sc = A.ints(list(ash)), A.sizes(list(ast)), A.ints(list(bsh)), A.sizes(list(bst)), A.ints([m, n])
+
+        def launch(stream, r, da=da, db=db, sa=sa, sta=sta, sb=sb, stb=stb, sc=sc):
+            A.check(lib.pt_matmul(da.ptr, db.ptr, c.ptr, A.FLOAT32, sa, sta, 2, sb, stb, 2, sc, 2, stream), "matmul")
+        t = GraphTimer(launch, reps=4)
+        t.run(2)
+        ms = t.run(max(2, steps))
+        t.close()
+        out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+    log("config-5 products: " + "  ".join(f"{k} {v['us']} us" for k, v in out.items()))
+    return out
+
+
+_VENDOR_MLP = r"""
+import json, torch
+torch.backends.cuda.matmul.allow_tf32 = False
+g = torch.Generator(device="cuda").manual_seed(5)
+SHAPES = SHAPES_HERE
+out = {}
+for name, (ash, ast, bsh, bst) in SHAPES.items():
+    def operand(shape, strides):
+        span = 1 + sum((d - 1) * s for d, s in zip(shape, strides))
+        base = torch.randn(span, device="cuda", generator=g) * 0.05
+        return torch.as_strided(base, shape, strides)
+    a, b = operand(ash, ast), operand(bsh, bst)
+    c = torch.empty(ash[0], bsh[1], device="cuda")
+    for _ in range(STEPS // 2 + 1):
+        torch.mm(a, b, out=c)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(STEPS):
+        torch.mm(a, b, out=c)
+    e1.record()
+    e1.synchronize()
+    out[name] = e0.elapsed_time(e1) / STEPS
+print(json.dumps({"ms": out}))
+"""
+
+
+def vendor_mlp_gemms(steps):
+    """torch.mm (hipBLASLt / rocBLAS) on the same five products, in a child
+    process: a comparison point only."""
+    import subprocess
+    code = _VENDOR_MLP.replace("STEPS", str(max(4, steps))).replace("SHAPES_HERE", repr(_MLP_GEMMS))
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
+    if proc.returncode != 0:
+        return {"error": proc.stderr.strip().splitlines()[-1] if proc.stderr.strip() else f"rc {proc.returncode}"}
+    r = json.loads(proc.stdout.strip().splitlines()[-1])
+    out = {k: round(v * 1e3, 1) for k, v in r["ms"].items()}
+    log("torch.mm on the config-5 products: " + "  ".join(f"{k} {v} us" for k, v in out.items()))
+    return {"us": out}
+
+
 def transfer_family(steps, nbytes=256 << 20):
     """Host <-> device transfers through pt_memcpy_h2d / pt_memcpy_d2h
     (tensor_transfer.c:45-65): a pageable numpy buffer (staged through the
@@ -577,6 +658,9 @@ def main():
     extra = {}
     if "mlp" in only:
         extra["mlp"] = mlp_family(max(1, args.steps // 2), args.warmup)
+        extra["mlp"]["products"] = mlp_gemms(args.steps)
+        if args.vendor:
+            extra["mlp"]["vendor_torch_mm"] = vendor_mlp_gemms(args.steps)
     if "eager" in only:
         extra["eager"] = eager_family(args.steps, args.warmup)
     if "transfer" in only:
