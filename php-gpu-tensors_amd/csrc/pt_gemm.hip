@@ -292,6 +292,11 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
 
     const int arow = wm * C::WTM + (lane & 31);
     const int brow = wn * C::WTN + (lane & 31);
+    // k-major A with two or four row blocks per wave: block i's row r is the
+    // wave's local row TM * r + i, so that one lane's values of all blocks at
+    // one k sit side by side in LDS and load as one 8- or 16-byte read
+    constexpr bool AIL = AKM && (TM == 2 || TM == 4);
+    const int arow_il = wm * C::WTM + TM * (lane & 31);
     const int khalf = (lane >> 5) * PK;
     // One k-slice feeds one MFMA per (i, j) block: 16 k for 16-bit operands,
     // 8 k (four 32x32x2 MFMAs) for fp32.  Fragments of slice s+1 are read
@@ -302,9 +307,27 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
     using Frag = typename FragT<DT>::type;
     Frag fa[2][TM], fb[2][TN];
     auto read_frags = [&](const S *sa, const S *sb, int slice, Frag (&ra)[TM], Frag (&rb)[TN]) {
+        if constexpr (AIL) {
+#pragma unroll
+            for (int e = 0; e < PK; e++) {
+                const S *src = sa + (slice * KS + khalf + e) * LDA + arow_il;
+                if constexpr (TM == 2) {
+                    const float2 t = *(const float2 *)src;
+                    ra[0][e] = t.x;
+                    ra[1][e] = t.y;
+                } else {
+                    const float4 t = *(const float4 *)src;
+                    ra[0][e] = t.x;
+                    ra[1][e] = t.y;
+                    ra[2][e] = t.z;
+                    ra[3][e] = t.w;
+                }
+            }
+        }
 #pragma unroll
         for (int i = 0; i < TM; i++) {
-            if constexpr (AKM) {
+            if constexpr (AIL) {
+            } else if constexpr (AKM) {
 #pragma unroll
                 for (int e = 0; e < PK; e++) ra[i][e] = sa[(slice * KS + khalf + e) * LDA + arow + i * 32];
             } else {
@@ -374,7 +397,8 @@ __device__ __forceinline__ void gemm_core(const GemmArgs &g,
             const int n = n0 + wn * C::WTN + j * 32 + col_l;
 #pragma unroll
             for (int e = 0; e < 16; e++) {
-                const int m = m0 + wm * C::WTM + i * 32 + (e >> 2) * 8 + row_l + (e & 3);
+                const int rho = (e >> 2) * 8 + row_l + (e & 3);  // row within the 32x32 block
+                const int m = m0 + wm * C::WTM + (AIL ? TM * rho + i : i * 32 + rho);
                 if ((!CHECK && !CLAMP) || (m < g.M && n < g.N)) {
                     if (Pb) Pb[(size_t)m * g.N + n] = acc[i][j][e];
                     else store_c<DT>(Cb, (size_t)m * g.N + n, acc[i][j][e]);
