@@ -298,10 +298,14 @@ def test_var_nonfinite_and_correction_errors(G):
     x = np.array([1.0, np.inf], np.float64)
     assert np.isnan(G.moments(x, O.F64)[0])
     # long rows (register-resident two-pass kernel): infinities poison too
-    xl = np.ones((2, 4096), np.float32)
+    xl = np.ones((5, 4096), np.float32)
     xl[0, 5] = np.inf
+    xl[2, 4095] = -np.inf
+    xl[3, 0] = np.nan
+    xl[4, 7], xl[4, 4000] = np.inf, -np.inf
     got = G.moments(xl, O.F32, 1)
     assert np.isnan(got[0]) and got[1] == 0.0
+    assert np.isnan(got[2]) and np.isnan(got[3]) and np.isnan(got[4])
     with pytest.raises(InvalidArgumentException):
         G.moments(np.zeros((0, 3), np.float32), O.F32)
     with pytest.raises(InvalidArgumentException):
