@@ -19,6 +19,7 @@
 #include <mutex>
 #include <string.h>
 #include <thread>
+#include <unistd.h>
 #include <vector>
 
 namespace pt {
@@ -31,7 +32,9 @@ namespace pt {
 // Parallel host memcpy: the caller copies the first part, PT_COPY_THREADS - 1
 // resident workers the others.  Workers start on first use and live until
 // the process ends (the pool is never destroyed, so no exit-time destructor
-// waits on them).  One copy runs at a time (the stager's lock).
+// waits on them).  One copy runs at a time (the stager's lock).  A child
+// made by fork() has no workers, only their record: it copies on the
+// calling thread.
 class CopyPool {
 public:
     void copy(char *dst, const char *src, size_t n)
@@ -39,8 +42,13 @@ public:
         const size_t part = ((n + PT_COPY_THREADS - 1) / PT_COPY_THREADS + 4095) & ~(size_t)4095;
         {
             std::lock_guard<std::mutex> lk(m_);
-            if (workers_.empty())
+            if (workers_.empty()) {
+                owner_ = getpid();
                 for (int w = 1; w < PT_COPY_THREADS; w++) workers_.emplace_back(&CopyPool::work, this, w);
+            } else if (owner_ != getpid()) {
+                memcpy(dst, src, n);
+                return;
+            }
             for (int p = 0; p < PT_COPY_THREADS; p++) {
                 const size_t off = std::min(n, p * part);
                 parts_[p] = Part{dst + off, src + off, std::min(part, n - off)};
@@ -80,6 +88,7 @@ private:
     Part parts_[PT_COPY_THREADS] = {};
     unsigned long generation_ = 0;
     int pending_ = 0;
+    pid_t owner_ = 0;  // process whose threads the workers are
 };
 
 // The ring of two pinned chunks and the events that mark their DMA done.
