@@ -949,7 +949,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         // for 128x64 tiles at two workgroups per CU)
         const int mid32 = TILE_128x128_W8;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
-                   ? (dtype == PT_FLOAT32 ? TILE_256x128_W8
+                   ? (dtype == PT_FLOAT32 ? TILE_256x256
                       : dtype == PT_BFLOAT16 ? TILE_RING_DEFAULT : TILE_RING_DEFAULT_F16)
                    : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? mid32 : TILE_128x128)
                                                 : TILE_64x64;

@@ -73,7 +73,7 @@ def _ints(shape, seed, lo=-8, hi=8):
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
 
 
-@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 8, 9, 10, 11, 12, 13])
+@pytest.mark.parametrize("tile", [-1, 0, 1, 2, 3, 5, 8, 9, 10, 11, 12, 13])
 @pytest.mark.parametrize("dt", [O.F32, O.BF16, O.F16], ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("bmnk", SHAPES, ids=str)
 def test_matmul_integer_exact(A, bmnk, dt, tile):
@@ -85,6 +85,32 @@ def test_matmul_integer_exact(A, bmnk, dt, tile):
         a, b = O.to_storage(a32, dt), O.to_storage(b32, dt)
         got = run(A, a, b, dt)
         assert np.array_equal(got, ref(a, b, dt))
+    finally:
+        A.load().pt_matmul_set_tile(-1)
+
+
+@pytest.mark.parametrize("tile", [-1, 0, 1, 3, 5, 9, 10, 11])
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("bmnk", [(2, 512, 512, 256), (1, 256, 768, 96), (1, 300, 260, 130)], ids=str)
+def test_matmul_fp32_tiles_layouts(A, bmnk, layout, tile):
+    """fp32 tiles over every operand layout: transposed A and row-major B stage
+    k-major in LDS, where the row blocks of a wave interleave for wide
+    fragment reads.  Exact on integer-valued operands, whole and edge tiles."""
+    b_, m, n, k = bmnk
+    A.load().pt_matmul_set_tile(tile)
+    try:
+        a = _ints((b_, m, k), seed=m + 11 * k)
+        b = _ints((b_, k, n), seed=n + 13 * k)
+        expect = ref(a, b, O.F32)
+        kw = {}
+        a_in, b_in = a, b
+        if layout[0] == "T":   # A as the transposed view of a [b, k, m] buffer
+            a_in = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+            kw.update(shape_a=(b_, m, k), strides_a=[m * k, 1, m])
+        if layout[1] == "T":   # B as the transposed view of a [b, n, k] buffer
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+            kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
+        assert np.array_equal(run(A, a_in, b_in, O.F32, **kw), expect)
     finally:
         A.load().pt_matmul_set_tile(-1)
 
