@@ -72,6 +72,39 @@ def test_staged_transfers_round_trip(lib, nbytes, offset):
         A.check(lib.pt_host_free_pinned(pinned.value), "free pinned")
 
 
+def test_staged_transfers_from_several_threads(lib):
+    """Four host threads move pageable buffers through the one staging ring
+    at the same time (the foreign calls run without the interpreter lock):
+    the transfers take turns and every byte arrives."""
+    import threading
+    nbytes = (9 << 20) + 123
+    errors = []
+
+    def worker(seed):
+        try:
+            rng = np.random.default_rng(seed)
+            dev = A.DeviceBuffer(nbytes)
+            for _ in range(3):
+                host = rng.integers(0, 256, nbytes, dtype=np.uint8)
+                A.check(lib.pt_memcpy_h2d(dev.ptr, host.ctypes.data, nbytes, None), "h2d")
+                back = np.empty(nbytes, np.uint8)
+                A.check(lib.pt_memcpy_d2h(back.ctypes.data, dev.ptr, nbytes, None), "d2h")
+                if not np.array_equal(back, host):
+                    errors.append(f"thread {seed}: bytes differ")
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(f"thread {seed}: {e}")
+
+    before = A.backend_info().staged_copies
+    threads = [threading.Thread(target=worker, args=(s,)) for s in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not any(t.is_alive() for t in threads), "a transfer thread did not finish"
+    assert not errors, errors
+    assert A.backend_info().staged_copies - before == 4 * 3 * 2
+
+
 def test_pool_reuse_and_info(lib):
     bufs = [A.DeviceBuffer(s) for s in (1 << 10, 1 << 20, 1 << 24, 3, 1 << 16)]
     for b in bufs:
