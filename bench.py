@@ -58,6 +58,24 @@ GEMM_KERNELS = {"mfma-lds-ring": "k_gemm_ring", "mfma-direct-lds": "k_gemm_direc
 MALL_BYTES = 256 << 20
 
 
+# Untimed warm-up per timed kernel, in milliseconds of its own work.  The
+# MI355X shader clock rises over the first tens of milliseconds of sustained
+# load (three consecutive 40-launch windows of the bf16 config-4 GEMM ran at
+# 564, 508 and 496 us per launch), so a fixed count of a few launches would
+# time the ramp rather than the steady state.  The vendor legs use the same rule.
+WARM_MS = 100.0
+
+
+def warm_up(run, calls, launches_per_call=1):
+    """Call run(calls) (which returns ms per launch) until WARM_MS of work has
+    run, and at least once."""
+    spent = 0.0
+    while True:
+        spent += run(calls) * calls * launches_per_call
+        if spent >= WARM_MS:
+            return
+
+
 class GraphTimer:
     """Capture `launch()` `reps` times into a graph on a private stream and
     time replays with HIP events recorded on that stream."""
@@ -138,7 +156,7 @@ def reduce_family(steps, warmup):
     results = {}
     for kind in ("sum", "mean", "max", "argmax", "var", "softmax", "layernorm"):
         t = GraphTimer(mk(kind), reps=2 * replicas)
-        t.run(max(1, warmup))
+        warm_up(t.run, max(1, warmup), t.reps)
         ms = t.run(max(1, steps))
         t.close()
         b = row_bytes if kind in ("softmax", "layernorm") else red_bytes
@@ -155,7 +173,7 @@ def reduce_family(steps, warmup):
     def copy(stream, r):
         A.check(lib.pt_memcpy_d2d(big.ptr, xs[r % replicas].ptr, nbytes, stream), "copy")
     t = GraphTimer(copy, reps=2 * replicas)
-    t.run(max(1, warmup))
+    warm_up(t.run, max(1, warmup), t.reps)
     ms = t.run(max(1, steps))
     t.close()
     copy_gbs = row_bytes / (ms * 1e-3) / 1e9
@@ -198,7 +216,7 @@ def fused_family(steps, warmup, replays=100):
         A.check(lib.pt_event_elapsed_ms(ev0, ev1, ctypes.byref(ms)), "elapsed")
         return ms.value / count
 
-    timed(max(1, warmup) * 10)
+    warm_up(timed, max(1, warmup) * 10)
     samples = sorted(timed(replays) for _ in range(max(1, steps // 5)))
     ms = samples[len(samples) // 2]
     # FusionGraph::run as the reference calls it: bind, replay, synchronize per call
@@ -247,7 +265,7 @@ def eager_family(steps, warmup):
     results = {}
     for name, (fn, nbytes, kernel) in ops.items():
         tm = GraphTimer(lambda stream, r, fn=fn: A.check(fn(stream), name), reps=4)
-        tm.run(max(1, warmup))
+        warm_up(tm.run, max(1, warmup), tm.reps)
         ms = tm.run(max(1, steps))
         tm.close()
         gbs = nbytes / (ms * 1e-3) / 1e9
@@ -319,7 +337,7 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
                                   stream), "matmul")
 
         t = GraphTimer(launch, reps=1)
-        t.run(max(1, warmup))
+        warm_up(t.run, max(1, warmup))
         ms = t.run(max(1, steps))
         t.close()
         path = A.backend_info().last_matmul.decode()
@@ -340,7 +358,7 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
 # a comparison point on the same box, run in a child process so that the
 # library and torch never share one process.  Not the product path.
 _VENDOR_GEMM = r"""
-import json, torch
+import json, time, torch
 bsz, m, n, k = 32, 2048, 2048, 2048
 g = torch.Generator(device="cuda").manual_seed(4)
 out = {}
@@ -348,8 +366,14 @@ for name, dt in (("bf16", torch.bfloat16), ("fp16", torch.float16), ("fp32", tor
     a = (torch.randn(bsz, m, k, device="cuda", generator=g) * 0.02).to(dt).contiguous()
     b = (torch.randn(bsz, k, n, device="cuda", generator=g) * 0.02).to(dt).contiguous()
     c = torch.empty(bsz, m, n, device="cuda", dtype=dt)
-    for _ in range(STEPS // 2 + 1):
-        torch.bmm(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while True:  # warm-up: at least WARM_MS of work, as for this build's kernels
+        for _ in range(STEPS // 2 + 1):
+            torch.bmm(a, b, out=c)
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= WARM_MS_HERE:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
@@ -367,7 +391,7 @@ print(json.dumps({"torch": torch.__version__, "ms": out,
 def vendor_gemm(steps):
     """Time torch.bmm on the config-4 shapes in a child process."""
     import subprocess
-    code = _VENDOR_GEMM.replace("STEPS", str(max(2, steps)))
+    code = _VENDOR_GEMM.replace("STEPS", str(max(2, steps))).replace("WARM_MS_HERE", repr(WARM_MS))
     proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
     if proc.returncode != 0:
         return {"error": proc.stderr.strip().splitlines()[-1] if proc.stderr.strip() else f"rc {proc.returncode}"}
@@ -407,7 +431,7 @@ def mlp_family(steps, warmup):
         A.check(lib.pt_event_elapsed_ms(ev0, ev1, ctypes.byref(ms)), "elapsed")
         return ms.value / count
 
-    timed(max(1, warmup))
+    warm_up(timed, max(1, warmup))
     ms = timed(max(1, steps))
     # eager: the same step through the Python-level autograd, synchronized
     A.synchronize()
@@ -461,7 +485,7 @@ def mlp_gemms(steps):
         def launch(stream, r, da=da, db=db, sa=sa, sta=sta, sb=sb, stb=stb, sc=sc):
             A.check(lib.pt_matmul(da.ptr, db.ptr, c.ptr, A.FLOAT32, sa, sta, 2, sb, stb, 2, sc, 2, stream), "matmul")
         t = GraphTimer(launch, reps=4)
-        t.run(2)
+        warm_up(t.run, 2, t.reps)
         ms = t.run(max(2, steps))
         t.close()
         out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
@@ -470,7 +494,7 @@ def mlp_gemms(steps):
 
 
 _VENDOR_MLP = r"""
-import json, torch
+import json, time, torch
 torch.backends.cuda.matmul.allow_tf32 = False
 g = torch.Generator(device="cuda").manual_seed(5)
 SHAPES = SHAPES_HERE
@@ -482,8 +506,14 @@ for name, (ash, ast, bsh, bst) in SHAPES.items():
         return torch.as_strided(base, shape, strides)
     a, b = operand(ash, ast), operand(bsh, bst)
     c = torch.empty(ash[0], bsh[1], device="cuda")
-    for _ in range(STEPS // 2 + 1):
-        torch.mm(a, b, out=c)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while True:  # warm-up: at least WARM_MS of work, as for this build's kernels
+        for _ in range(STEPS // 2 + 1):
+            torch.mm(a, b, out=c)
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= WARM_MS_HERE:
+            break
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     e0.record()
@@ -500,7 +530,8 @@ def vendor_mlp_gemms(steps):
     """torch.mm (hipBLASLt / rocBLAS) on the same five products, in a child
     process: a comparison point only."""
     import subprocess
-    code = _VENDOR_MLP.replace("STEPS", str(max(4, steps))).replace("SHAPES_HERE", repr(_MLP_GEMMS))
+    code = (_VENDOR_MLP.replace("STEPS", str(max(4, steps))).replace("SHAPES_HERE", repr(_MLP_GEMMS))
+            .replace("WARM_MS_HERE", repr(WARM_MS)))
     proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=600)
     if proc.returncode != 0:
         return {"error": proc.stderr.strip().splitlines()[-1] if proc.stderr.strip() else f"rc {proc.returncode}"}
