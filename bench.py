@@ -49,7 +49,7 @@ PMC_TRAFFIC_BYTES = {
     "reduce:sum": 134_516_736, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
     "reduce:argmax": 134_521_856, "reduce:var": 134_542_336, "reduce:softmax": 268_545_024,
     "reduce:layernorm": 269_121_536, "fused:tanh_x_plus_y_z": 1_610_682_496,
-    "gemm:bf16": 1_078_208_768, "gemm:fp16": 1_083_626_048, "gemm:fp32": 2_147_819_904,
+    "gemm:bf16": 1_075_905_024, "gemm:fp16": 1_083_517_888, "gemm:fp32": 2_147_847_040,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol

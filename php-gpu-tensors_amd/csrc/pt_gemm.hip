@@ -725,11 +725,11 @@ enum GemmTile {
     // 4-wave LDS-ring kernels (k_gemm_ring): BK x stages
     TILE_RING_FIRST = 14, TILE_RING_LAST = 31,  // variants 0..17 of gemm_ring_variants()
     TILE_COUNT = 32,
-    // large bf16 products: 4 waves, BK 32, five stages, loads spread over
-    // the MFMA slices (606 us on config 4 against 620 us for BK 64 x two
-    // stages and 693 us for the direct kernel); large fp16 products: the same
-    // ring with 8 waves (673 us against 701 us with 4 waves, 706 us direct)
-    TILE_RING_DEFAULT = TILE_RING_FIRST + 12, TILE_RING_DEFAULT_F16 = TILE_RING_FIRST + 16
+    // large bf16 and fp16 products: the ring with 8 waves, BK 32, five
+    // stages, loads spread over the MFMA slices.  At steady state (after the
+    // clock's ramp) on config 4: bf16 485 us against 494 us with 4 waves,
+    // fp16 549 us against 589 us.
+    TILE_RING_DEFAULT = TILE_RING_FIRST + 16, TILE_RING_DEFAULT_F16 = TILE_RING_DEFAULT
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
@@ -1119,7 +1119,7 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
                                 TILE_128x64_W4M2_K2};
     static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
                                 TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8, TILE_RING_DEFAULT,
-                                TILE_RING_DEFAULT_F16, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};
+                                TILE_RING_FIRST + 12, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};
     const int *cands = dtype == PT_FLOAT32 ? kFp32 : kHalf;
     const int ncand = dtype == PT_FLOAT32 ? (int)(sizeof(kFp32) / sizeof(int)) : (int)(sizeof(kHalf) / sizeof(int));
     hipStream_t s = stream_of(stream);
