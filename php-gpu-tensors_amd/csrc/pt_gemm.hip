@@ -470,24 +470,42 @@ __global__ __launch_bounds__(64 * WM * WN, MINW) void k_gemm(GemmArgs g)
 
 // Split-K epilogue: C = sum of the K-chunk partials, in chunk order, rounded
 // once to the output dtype.
-template <int DT>
+// Sum of the split-K partials [ksplit][count] in chunk order, rounded once.
+// V adjacent outputs per thread (16-byte loads when V = 4); eight chunks'
+// loads are in flight at a time, predicated past the last chunk, and their
+// additions stay in order (a chunk past the end is skipped, not added as 0,
+// so that a -0.0 sum keeps its sign).
+template <int DT, int V>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float *__restrict__ partial, void *__restrict__ c,
                                                        size_t count, int ksplit)
 {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
     if (i >= count) return;
-    float acc = partial[i];
-    int k = 1;
-    // sixteen partials in flight per thread; the additions stay in chunk order
-    for (; k + 16 <= ksplit; k += 16) {
-        float v[16];
+    float acc[V];
+    auto load = [&](int k, float (&v)[V]) {
+        const float *p = partial + (size_t)k * count + i;
+        if constexpr (V == 4) {
+            const float4 t = *(const float4 *)p;
+            v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+        } else {
 #pragma unroll
-        for (int u = 0; u < 16; u++) v[u] = partial[(size_t)(k + u) * count + i];
+            for (int e = 0; e < V; e++) v[e] = p[e];
+        }
+    };
+    load(0, acc);
+    for (int k = 1; k < ksplit; k += 8) {
+        float v[8][V];
 #pragma unroll
-        for (int u = 0; u < 16; u++) acc += v[u];
+        for (int u = 0; u < 8; u++)
+            if (k + u < ksplit) load(k + u, v[u]);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (k + u < ksplit)
+#pragma unroll
+                for (int e = 0; e < V; e++) acc[e] += v[u][e];
     }
-    for (; k < ksplit; k++) acc += partial[(size_t)k * count + i];
-    store_c<DT>(c, i, acc);
+#pragma unroll
+    for (int e = 0; e < V; e++) store_c<DT>(c, i + e, acc[e]);
 }
 
 // ------------------------------------------- direct-to-LDS 16-bit kernel
@@ -1075,12 +1093,20 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     if (g.ksplit > 1) {
         hipError_t e1 = hipGetLastError();
         const size_t count = (size_t)batch * g.M * g.N;
-        const unsigned blocks = (unsigned)((count + 255) / 256);
+        // four outputs per thread when whole 16-byte packs of every chunk line up
+        const bool v4 = count % 4 == 0 && ((uintptr_t)g.partial & 15u) == 0;
+        const unsigned blocks = (unsigned)(((v4 ? count / 4 : count) + 255) / 256);
+#define PT_SPLITK_SUM(DTV)                                                                          \
+    do {                                                                                            \
+        if (v4) k_splitk_reduce<DTV, 4><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit);     \
+        else k_splitk_reduce<DTV, 1><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit);        \
+    } while (0)
         switch (dtype) {
-        case PT_BFLOAT16: k_splitk_reduce<PT_BFLOAT16><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
-        case PT_FLOAT16: k_splitk_reduce<PT_FLOAT16><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
-        default: k_splitk_reduce<PT_FLOAT32><<<blocks, 256, 0, s>>>(g.partial, c, count, g.ksplit); break;
+        case PT_BFLOAT16: PT_SPLITK_SUM(PT_BFLOAT16); break;
+        case PT_FLOAT16: PT_SPLITK_SUM(PT_FLOAT16); break;
+        default: PT_SPLITK_SUM(PT_FLOAT32); break;
         }
+#undef PT_SPLITK_SUM
         hipError_t e2 = hipGetLastError();
         scratch_free(g.partial, s);
         PT_TRY(check_hip(e1, "matmul (split-K partials)"));
