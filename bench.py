@@ -336,8 +336,10 @@ def gemm_family(steps, warmup, dtypes=("bf16", "fp16", "fp32")):
             A.check(lib.pt_matmul(da.ptr, db.ptr, dc.ptr, dt, shp, st, 3, shp, st, 3, shp, 3,
                                   stream), "matmul")
 
-        t = GraphTimer(launch, reps=1)
-        warm_up(t.run, max(1, warmup))
+        # four launches per graph, as the other families capture several: the
+        # GPU leaves a few microseconds between two graph launches
+        t = GraphTimer(launch, reps=4)
+        warm_up(t.run, max(1, warmup), 4)
         ms = t.run(max(1, steps))
         t.close()
         path = A.backend_info().last_matmul.decode()

@@ -160,6 +160,10 @@ struct Plan {
     const char *incompatibility = nullptr;
     pt_graph_t graph = nullptr;
     std::vector<void *> graph_ptrs;  // pointers the captured graph was built with
+    // FusionGraph::replay: the steps captured kReplayCopies times in a row
+    // into one graph, for the buffers in batch_ptrs
+    pt_graph_t batch_graph = nullptr;
+    std::vector<void *> batch_ptrs;
     // buffer reuse: item index -> storage kept between runs
     std::unordered_map<int, std::shared_ptr<Storage>> cache;
     // statistics (FusionGraph::getStats, fusion.c:723-772)
@@ -1607,6 +1611,47 @@ static bool capture_steps(Plan &p, std::vector<TensorP> &vals, bool natives, boo
 static bool collect_outputs(Plan &p, std::vector<TensorP> &vals, std::vector<TensorP> &outs, uint64_t t0,
                             uint64_t t1);
 
+// Executions of one FusionGraph::replay call that share a graph launch.  The
+// GPU leaves a gap of several microseconds between two graph launches on a
+// stream and none between kernels inside one graph, so a replay of many
+// executions launches a graph that holds this many copies of the steps.
+static constexpr int kReplayCopies = 8;
+
+// Capture the steps `copies` times in a row into `p.batch_graph`, for the
+// buffers of `p.graph` (plans without native steps: their scratch is handed
+// out once per capture).  Each copy forks from and joins the capture stream,
+// so copy c + 1 starts after every branch of copy c has ended.
+static bool capture_copies(Plan &p, std::vector<TensorP> &vals, int copies)
+{
+    std::vector<pt_stream_t> streams;
+    if (!branch_streams(streams)) return false;  // before the capture begins
+    if (p.batch_graph) {
+        pt_graph_destroy(p.batch_graph);
+        p.batch_graph = nullptr;
+        p.batch_ptrs.clear();
+    }
+    if (!check_status(pt_graph_begin_capture(nullptr), "Graph capture failed")) return false;
+    std::vector<pt_event_t> events;
+    struct Release {
+        std::vector<pt_event_t> &e;
+        ~Release()
+        {
+            for (pt_event_t x : e) pt_event_destroy(x);
+        }
+    } release{events};
+    bool ok = true;
+    for (int c = 0; c < copies && ok; c++) ok = run_steps_branched(p, vals, events);
+    if (!ok) {
+        pt_stream_set_current(nullptr);
+        pt_graph_t scrap = nullptr;
+        if (pt_graph_end_capture(nullptr, &scrap) == PT_OK && scrap) pt_graph_destroy(scrap);
+        return false;
+    }
+    if (!check_status(pt_graph_end_capture(nullptr, &p.batch_graph), "Graph instantiation failed")) return false;
+    p.batch_ptrs = p.graph_ptrs;
+    return true;
+}
+
 // A plan with indexed native steps: clear the plan's validation record, run
 // the steps with the indexed natives recording into it, then read it back
 // (the execution's one synchronization) and raise the first invalid index
@@ -1644,8 +1689,14 @@ static bool execute_indexed(Plan &p, std::vector<TensorP> &vals, std::vector<Ten
     return collect_outputs(p, vals, outs, t0, t1);
 }
 
-static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<TensorP> &outs, bool wait)
+// `copies` == kReplayCopies (FusionGraph::replay): when the plan runs from
+// its captured graph and has no native steps, that many executions run in a
+// row on the same buffers through one graph launch.  `*ran_copies` is set to the
+// number of executions done (1 otherwise).
+static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<TensorP> &outs, bool wait,
+                    int copies = 1, int *ran_copies = nullptr)
 {
+    if (ran_copies) *ran_copies = 1;
     uint64_t t0 = now_ns();
     std::vector<TensorP> vals(p.items.size());
     for (size_t i = 0; i < p.items.size(); i++) {
@@ -1685,7 +1736,13 @@ static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<Ten
                 ran = true;
             }
         }
-        if (!ran) {
+        if (!ran && copies == kReplayCopies && !native_present) {
+            if ((!p.batch_graph || p.batch_ptrs != p.graph_ptrs) && !capture_copies(p, vals, copies)) return false;
+            if (!check_status(pt_graph_launch(p.batch_graph, nullptr), "Graph launch failed")) return false;
+            p.graph_launches += copies;
+            p.executions += copies - 1;
+            if (ran_copies) *ran_copies = copies;
+        } else if (!ran) {
             if (!check_status(pt_graph_launch(p.graph, nullptr), "Graph launch failed")) return false;
             p.graph_launches++;
         }
@@ -1951,10 +2008,14 @@ int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int coun
     std::vector<TensorP> ins, outs;
     if (!bind(p, inputs, ninputs, ins)) return -1;
     // outputs are dropped between replays, so every replay reuses the same
-    // buffers and the captured graph; one synchronization at the end
-    for (int i = 0; i < count; i++) {
-        if (!execute(p, ins, outs, false)) return -1;
+    // buffers and the captured graph; whole groups of kReplayCopies go
+    // through one graph launch; one synchronization at the end
+    for (int i = 0; i < count;) {
+        int ran = 1;
+        const int n = count - i >= kReplayCopies ? kReplayCopies : 1;
+        if (!execute(p, ins, outs, false, n, &ran)) return -1;
         outs.clear();
+        i += ran;
     }
     if (!check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed")) return -1;
     p.synchronizations++;
@@ -2132,6 +2193,7 @@ void phpt_graph_release(phpt_graph *g)
     Plan &p = *g->plan;
     if (p.pending) pt_stream_synchronize(nullptr);
     if (p.graph) pt_graph_destroy(p.graph);
+    if (p.batch_graph) pt_graph_destroy(p.batch_graph);
     delete g->plan;
     delete g;
 }

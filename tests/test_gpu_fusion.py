@@ -413,6 +413,46 @@ def test_native_plan_with_workspace_replays_from_graph():
             np.testing.assert_array_equal(g.toBits(), e.toBits())
     st = graph.getStats()
     assert st["cudaGraphCompatible"] == 1 and st["graphLaunches"] == 3
+    # replays of a plan with native steps go one graph launch at a time
+    graph.replay(9, a, b)
+    st = graph.getStats()
+    assert st["graphLaunches"] == 12 and st["executions"] == 13
+    for g, e in zip(graph.run(a, b), eager):
+        np.testing.assert_array_equal(g.toBits(), e.toBits())
+
+
+@pytest.mark.parametrize("count", [1, 7, 8, 9, 17])
+def test_replay_groups_of_copies_keep_results_and_stats(count):
+    """FusionGraph::replay launches whole groups of eight executions of a
+    plan without native steps as one graph that holds eight copies of its
+    steps (here three kernels on parallel branches).  Every execution is
+    counted as a graph launch, a run after the replays gives the eager
+    results bit for bit, and replays with another input buffer capture both
+    graphs again, so that later runs follow the new input."""
+    r = np.random.default_rng(90 + count)
+    x = CudaArray.fromNumpy(r.standard_normal((1000, 33)).astype(np.float32))
+    y = CudaArray.fromNumpy(r.standard_normal((33,)).astype(np.float32))
+    z = CudaArray.fromNumpy(r.standard_normal((64, 7)).astype(np.float32))
+
+    def body(a, b, c):
+        return [(a * b + a).tanh(), (c * 2.0 - 1.0).abs(), (a - b).exp()]
+
+    graph = Fusion.compile(body, [x, y, z], cudaGraph=True)
+    assert len(graph.getPlan()) >= 2
+    st0 = graph.getStats()
+    graph.replay(count, x, y, z)
+    st1 = graph.getStats()
+    assert st1["graphLaunches"] - st0["graphLaunches"] == count
+    assert st1["executions"] - st0["executions"] == count
+    for rep in range(2):
+        for i, (o, e) in enumerate(zip(graph.run(x, y, z), body(x, y, z))):
+            assert np.array_equal(o.toBits(), e.toBits()), (rep, i)
+        (x * 3.0).sum().toNumpy()  # eager work between runs
+    x2 = CudaArray.fromNumpy(r.standard_normal((1000, 33)).astype(np.float32))
+    graph.replay(count, x2, y, z)
+    for i, (o, e) in enumerate(zip(graph.run(x2, y, z), body(x2, y, z))):
+        assert np.array_equal(o.toBits(), e.toBits()), i
+    assert graph.getStats()["graphLaunches"] - st1["graphLaunches"] == count + 3  # and three runs
 
 
 # ------------------------------------------- dependent outputs (reference)
