@@ -392,6 +392,42 @@ def test_config4_full_size_sampled(A, dt):
             assert abs(g - exact) <= 1e-2 * max(abs(exact), scale / math.sqrt(k))
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16, O.F32], ids=["bf16", "f16", "f32"])
+def test_config4_full_size_every_output(A, dt):
+    """Every one of the 134 M outputs of config 4 (A,B [32,2048,2048]
+    N(0,0.02), seeds 4/5), so that every 256x256 tile, batch and XCD-remapped
+    workgroup is checked, against an fp32 product of the same rounded operands
+    on the host (numpy matmul, i.e. the BLAS sgemm; this library and torch do
+    not share a process).  The reference's own error is at most
+    K * 2^-24 = 1.2e-4 of |A|.|B| in the worst case, 3 % of the fp32 tolerance
+    and about half of the 16-bit floor, and a random walk of
+    sqrt(K) * 2^-24 = 2.7e-6 of it in practice.  Tolerances: fp32
+    1e-4 * sqrt(K) * (|A|.|B|), bf16 / fp16 1e-2 relative with the floor
+    (|A|.|B|) / sqrt(K) of the sampled test above.  A transposed operand, a
+    wrong tile origin or a skipped K step moves outputs by O(|C|) and fails."""
+    from phptensors import synthetic
+    shape, k = (32, 2048, 2048), 2048
+    a = O.to_storage(synthetic.normal(shape, 0.0, 0.02, seed=4), dt)
+    b = O.to_storage(synthetic.normal(shape, 0.0, 0.02, seed=5), dt)
+    got = O.from_storage(run(A, a, b, dt), dt).astype(np.float32)
+    af = O.from_storage(a, dt).astype(np.float32)
+    bf = O.from_storage(b, dt).astype(np.float32)
+    del a, b
+    ref32 = np.matmul(af, bf)
+    scale = np.matmul(np.abs(af), np.abs(bf))
+    del af, bf
+    if dt == O.F32:
+        bound = np.float32(1e-4 * math.sqrt(k)) * scale
+    else:
+        bound = np.float32(1e-2) * np.maximum(np.abs(ref32), scale / np.float32(math.sqrt(k)))
+    del scale
+    err = np.abs(got - ref32)
+    bad = int(np.count_nonzero(err > bound))
+    worst = float(np.max(err / bound))
+    assert np.isfinite(got).all()
+    assert bad == 0, f"{bad} outputs outside tolerance (worst {worst:.3g} of the bound)"
+
+
 # ------------------------------------------------ precision policy and tuning
 def test_matmul_precision_reference():
     """matmul_precision.phpt:14-57 on a device without TF32: strict fp32 is the
