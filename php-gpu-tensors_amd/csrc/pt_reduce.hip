@@ -654,22 +654,9 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
     // HBM latency overlaps the barriers and stores of the current row (only
     // while two rows and gamma/beta fit the register budget)
     constexpr bool PF = NCH * VEC <= 32;
-    CT nx[NCH][VEC];
-    if constexpr (PF) load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, nx);
-    for (; row < rows; row += row_step) {
-        CT *y = out + row * (size_t)n;
-        CT v[NCH][VEC];
-        if constexpr (PF) {
-#pragma unroll
-            for (int c = 0; c < NCH; c++)
-#pragma unroll
-                for (int k = 0; k < VEC; k++) v[c][k] = nx[c][k];
-            if (row + row_step < rows)
-                load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + (row + row_step) * (size_t)n, n, wr, lane,
-                                                 (CT)0, nx);
-        } else {
-            load_row<DT, VEC, NCH, WPR, LNT>((const S *)xin + row * (size_t)n, n, wr, lane, (CT)0, v);
-        }
+    // one row: reductions, normalisation, gamma / beta, store
+    auto process = [&](CT (&v)[NCH][VEC], size_t r) {
+        CT *y = out + r * (size_t)n;
         CT s = 0;
 #pragma unroll
         for (int c = 0; c < NCH; c++)
@@ -720,6 +707,28 @@ __global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ 
             finish([&](CT a) { return a / dev; });
         }
         store_row<VEC, NCH, WPR, SNT>(y, n, wr, lane, full, v);
+    };
+    auto src = [&](size_t r) { return (const S *)xin + r * (size_t)n; };
+    if constexpr (PF) {
+        // two row buffers used in turn: the next row's loads land in one
+        // while the other is reduced, normalised and stored (no register
+        // copy between them)
+        CT b0[NCH][VEC], b1[NCH][VEC];
+        load_row<DT, VEC, NCH, WPR, LNT>(src(row), n, wr, lane, (CT)0, b0);
+        for (; row < rows; row += 2 * row_step) {
+            const size_t r1 = row + row_step;
+            if (r1 < rows) load_row<DT, VEC, NCH, WPR, LNT>(src(r1), n, wr, lane, (CT)0, b1);
+            process(b0, row);
+            if (r1 >= rows) break;
+            if (r1 + row_step < rows) load_row<DT, VEC, NCH, WPR, LNT>(src(r1 + row_step), n, wr, lane, (CT)0, b0);
+            process(b1, r1);
+        }
+    } else {
+        for (; row < rows; row += row_step) {
+            CT v[NCH][VEC];
+            load_row<DT, VEC, NCH, WPR, LNT>(src(row), n, wr, lane, (CT)0, v);
+            process(v, row);
+        }
     }
 }
 
