@@ -1702,7 +1702,28 @@ static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS
     k_row_softmax_stream<DT, OS><<<(unsigned)rows, 256, 0, s>>>(x, n, ld, y);
 }
 
-static const int kLnBlocks = 256 * 8;
+// Grid of a row-walking kernel: two whole generations of the blocks that
+// fit on the device at once.  A partial last generation leaves CUs idle
+// while its blocks walk their rows: on config 2 the layerNorm walk took
+// 44.3-44.4 us with 2048 blocks (768 resident) and 43.3-43.4 us with 768,
+// 1536 or 3072.  The count is taken once per kernel, on the first device
+// that launches it (every device of a host is the same model here).
+template <auto K>
+static unsigned walk_grid(size_t rows)
+{
+    static const unsigned resident = [] {
+        int dev = 0, cus = 0, per_cu = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, K, 256, 0) != hipSuccess || per_cu < 1)
+            per_cu = 1;
+        (void)hipGetLastError();  // a failed query is not the launch's error
+        return (unsigned)(per_cu * cus);
+    }();
+    const size_t b = 2 * (size_t)resident;
+    return (unsigned)(rows < b ? rows : b);
+}
 
 template <int DT, typename CT>
 static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, const CT *g,
@@ -1713,18 +1734,29 @@ static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, con
     bool vec = n % V == 0 && aligned16(x) && aligned16(y) && (!g || aligned16(g)) &&
                (!b || aligned16(b));
     int chunks = (n + 64 * V - 1) / (64 * V);
-    // block-per-row kernels walk rows: 8 blocks per CU share the rows
-    grid1 = dim3((unsigned)(rows < (size_t)kLnBlocks ? rows : (size_t)kLnBlocks));
     if (vec) {
         switch (chunks) {
         case 1: k_row_layernorm<DT, V, 1, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
         case 2: k_row_layernorm<DT, V, 2, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
         case 3: case 4: k_row_layernorm<DT, V, 4, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
         default:
-            if (chunks <= 8) { k_row_layernorm<DT, V, 2, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
-            if (chunks <= 16) { k_row_layernorm<DT, V, 4, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
+            // block-per-row kernels walk the rows (walk_grid blocks)
+            if (chunks <= 8) {
+                constexpr auto k = k_row_layernorm<DT, V, 2, 4, CT>;
+                k<<<walk_grid<k>(rows), block, 0, s>>>(x, rows, n, eps, g, b, y);
+                return;
+            }
+            if (chunks <= 16) {
+                constexpr auto k = k_row_layernorm<DT, V, 4, 4, CT>;
+                k<<<walk_grid<k>(rows), block, 0, s>>>(x, rows, n, eps, g, b, y);
+                return;
+            }
             // (gamma and beta stay in registers too: 8 chunks per lane at most)
-            if (chunks <= 32) { k_row_layernorm<DT, V, 8, 4, CT><<<grid1, block, 0, s>>>(x, rows, n, eps, g, b, y); return; }
+            if (chunks <= 32) {
+                constexpr auto k = k_row_layernorm<DT, V, 8, 4, CT>;
+                k<<<walk_grid<k>(rows), block, 0, s>>>(x, rows, n, eps, g, b, y);
+                return;
+            }
             break;
         }
     }
