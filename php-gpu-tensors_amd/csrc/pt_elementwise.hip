@@ -379,9 +379,13 @@ __global__ __launch_bounds__(256) void k_unary(const void *__restrict__ x, int d
     }
 }
 
+// OPC >= 0: the op fixed at compile time (the per-element dispatch folds
+// away); OPC < 0: the op comes from `op`.
+template <int OPC>
 __global__ __launch_bounds__(256) void k_unary_f32_contig(const float *__restrict__ x,
-                                                          float *__restrict__ out, int op, long long n)
+                                                          float *__restrict__ out, int op_arg, long long n)
 {
+    const int op = OPC >= 0 ? OPC : op_arg;
     long long i = ((long long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
     const long long stride = (long long)gridDim.x * blockDim.x * 4;
     for (; i < n; i += stride) {
@@ -640,7 +644,13 @@ pt_status pt_unary(const void *input, int dtype, const size_t *strides, size_t o
     const char *px = (const char *)input + offset * dtype_size(dtype);
     bool contig = s.ndims <= 1 && (s.ndims == 0 || s.sa[0] == 1);
     if (contig && dtype == PT_FLOAT32 && ((uintptr_t)px & 15) == 0 && ((uintptr_t)out & 15) == 0) {
-        k_unary_f32_contig<<<grid_for(s.total, 4), 256, 0, st_>>>((const float *)px, (float *)out, op, s.total);
+        const unsigned g = grid_for(s.total, 4);
+        if (op == PT_OP_TANH)
+            k_unary_f32_contig<PT_OP_TANH><<<g, 256, 0, st_>>>((const float *)px, (float *)out, op, s.total);
+        else if (op == PT_OP_EXP)
+            k_unary_f32_contig<PT_OP_EXP><<<g, 256, 0, st_>>>((const float *)px, (float *)out, op, s.total);
+        else
+            k_unary_f32_contig<-1><<<g, 256, 0, st_>>>((const float *)px, (float *)out, op, s.total);
     } else {
         EwShape32 s32;
         const bool i32 = to32(s, s32);
