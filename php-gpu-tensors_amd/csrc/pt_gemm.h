@@ -99,11 +99,13 @@ __device__ __forceinline__ int swz_k(int row, int cpr)
     return cpr == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
-// 4-wave LDS-ring kernel for 16-bit operands (pt_gemm_ring.hip).  A variant
-// is a (K step, stages, tile width, workgroups per CU) shape; every variant
-// needs M % 256 == 0, N % tile width == 0 and K a multiple of gemm_ring_kmul.
+// LDS-ring kernels for 16-bit operands (pt_gemm_ring.hip).  A variant is a
+// (K step, stages, tile width, workgroups per CU, schedule, waves, kind)
+// shape; every variant needs M % 256 == 0, N % tile width == 0 and K a
+// multiple of gemm_ring_kmul.
 // b_row: B is n-contiguous (else k-contiguous).
 int gemm_ring_variants();
+int gemm_ring_kind(int variant);  // 0 k_gemm_ring, 1 k_gemm_pp, 2 k_gemm_wl
 int gemm_ring_bn(int variant);
 int gemm_ring_bk(int variant);
 int gemm_ring_kmul(int variant);

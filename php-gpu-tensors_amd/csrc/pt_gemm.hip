@@ -740,14 +740,17 @@ enum GemmTile {
     TILE_256x128_K2 = 4, TILE_256x256_K2 = 5, TILE_256x256_W4 = 6, TILE_256x256_W4_K2 = 7,
     TILE_256x256_DIRECT = 8, TILE_256x128_W8 = 9, TILE_128x128_W8 = 10, TILE_128x128_W8_K2 = 11,
     TILE_128x64_W4M2 = 12, TILE_128x64_W4M2_K2 = 13,
-    // 4-wave LDS-ring kernels (k_gemm_ring): BK x stages
-    TILE_RING_FIRST = 14, TILE_RING_LAST = 31,  // variants 0..17 of gemm_ring_variants()
-    TILE_COUNT = 32,
-    // large bf16 and fp16 products: the ring with 8 waves, BK 32, five
-    // stages, loads spread over the MFMA slices.  At steady state (after the
-    // clock's ramp) on config 4: bf16 485 us against 494 us with 4 waves,
-    // fp16 549 us against 589 us.
-    TILE_RING_DEFAULT = TILE_RING_FIRST + 16, TILE_RING_DEFAULT_F16 = TILE_RING_DEFAULT
+    // LDS-ring kernels (k_gemm_ring, k_gemm_pp, k_gemm_wl): variants 0..23
+    // of gemm_ring_variants()
+    TILE_RING_FIRST = 14, TILE_RING_LAST = 37,
+    TILE_COUNT = 38,
+    // large bf16 and fp16 products with K a multiple of 64: k_gemm_wl (the
+    // 8-wave ring with A in whole 128-byte lines).  Config 4 at steady state,
+    // alternating runs on one box: bf16 472-475 us against 488-490 us for the
+    // 8-wave ring with BK 32 x 5 stages, fp16 524 us against 532 us.  Other
+    // K keep that ring (TILE_RING_HALF).
+    TILE_RING_DEFAULT = TILE_RING_FIRST + 23, TILE_RING_DEFAULT_F16 = TILE_RING_DEFAULT,
+    TILE_RING_HALF = TILE_RING_FIRST + 16
 };
 struct TileInfo { int bm, bn, kmul; };
 static const TileInfo kTiles[TILE_COUNT] = {
@@ -755,6 +758,7 @@ static const TileInfo kTiles[TILE_COUNT] = {
     {256, 256, 1}, {256, 256, 2}, {256, 256, 2}, {256, 128, 1}, {128, 128, 1}, {128, 128, 2},
     {128, 64, 1}, {128, 64, 2}, {256, 256, 1}, {256, 256, 2}, {256, 256, 1}, {256, 256, 1},
     {256, 256, 1}, {256, 128, 1}, {256, 128, 1}, {256, 256, 2}, {256, 256, 1}, {256, 128, 1},
+    {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1},
     {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1},
     {256, 256, 1}, {256, 256, 1}};
 
@@ -968,6 +972,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         const int mid32 = TILE_128x128_W8;
         tile = (g.M >= 256 && g.N >= 256 && t256 >= 256)
                    ? (dtype == PT_FLOAT32 ? TILE_256x256
+                      : g.K % 64 != 0 ? TILE_RING_HALF
                       : dtype == PT_BFLOAT16 ? TILE_RING_DEFAULT : TILE_RING_DEFAULT_F16)
                    : (g.M >= 128 && g.N >= 128) ? (dtype == PT_FLOAT32 ? mid32 : TILE_128x128)
                                                 : TILE_64x64;
@@ -977,15 +982,17 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         tile = TILE_128x128;
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     if (tile >= TILE_RING_FIRST && tile <= TILE_RING_LAST) {
-        // 4-wave LDS-ring kernel: 16-bit operands, whole tiles (256 rows,
-        // 256 or 128 columns), K a multiple of gemm_ring_kmul, k-contiguous A,
-        // B k- or n-contiguous, 16-byte aligned rows and batch offsets
+        // LDS-ring kernels: 16-bit operands, whole tiles (256 rows, 256 or
+        // 128 columns), K a multiple of gemm_ring_kmul, k-contiguous A, B k-
+        // or n-contiguous, 16-byte aligned rows and batch offsets, and C
+        // aligned for the epilogue's 4-byte stores
         const int variant = tile - TILE_RING_FIRST;
         const int kmul = gemm_ring_kmul(variant), bn = gemm_ring_bn(variant);
         const bool b_row = g.b_sn == 1, b_col = g.b_sk == 1;
         const long long ldb = b_row ? g.b_sk : g.b_sn;
         bool ok = dtype != PT_FLOAT32 && g.a_sk == 1 && (b_row || b_col) && g.M % 256 == 0 && g.N % bn == 0 &&
-                  g.K % kmul == 0 && aligned(a) && aligned(b) && g.a_sm % 8 == 0 && ldb % 8 == 0;
+                  g.K % kmul == 0 && aligned(a) && aligned(b) && ((uintptr_t)c & 3u) == 0 && g.a_sm % 8 == 0 &&
+                  ldb % 8 == 0;
         for (int d = 0; d < g.nbd; d++)
             if (g.bsa[d] % 8 || g.bsb[d] % 8) ok = false;
         long long tiles = (long long)(g.M / 256) * (g.N / bn) * batch;
@@ -996,7 +1003,9 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
             launch_gemm_ring(g, dtype, b_row, variant, dim3((unsigned)tiles), s);
             PT_LAUNCH_CHECK("matmul");
             counters().mfma_gemm_calls++;
-            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "mfma-lds-ring%s", suffix);
+            static const char *kKindName[] = {"mfma-lds-ring", "mfma-lds-pingpong", "mfma-lds-wholeline"};
+            snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s%s",
+                     kKindName[gemm_ring_kind(variant)], suffix);
             return PT_OK;
         }
         tile = TILE_256x256_DIRECT;
@@ -1004,12 +1013,12 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     if (tile == TILE_256x256_DIRECT) {
         // direct-to-LDS kernel: 16-bit operands, whole 256x256 tiles, K a
         // multiple of 64, k-contiguous A, B k- or n-contiguous, 16-byte
-        // aligned rows and batch offsets
+        // aligned rows and batch offsets, C aligned for 4-byte stores
         const bool b_row = g.b_sn == 1, b_col = g.b_sk == 1;
         const long long ldb = b_row ? g.b_sk : g.b_sn;
         bool direct = dtype != PT_FLOAT32 && g.a_sk == 1 && (b_row || b_col) && g.M % 256 == 0 &&
-                      g.N % 256 == 0 && g.K % 64 == 0 && aligned(a) && aligned(b) && g.a_sm % 8 == 0 &&
-                      ldb % 8 == 0;
+                      g.N % 256 == 0 && g.K % 64 == 0 && aligned(a) && aligned(b) && ((uintptr_t)c & 3u) == 0 &&
+                      g.a_sm % 8 == 0 && ldb % 8 == 0;
         for (int d = 0; d < g.nbd; d++)
             if (g.bsa[d] % 8 || g.bsb[d] % 8) direct = false;
         long long tiles = (long long)(g.M / 256) * (g.N / 256) * batch;
@@ -1145,7 +1154,7 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
                                 TILE_128x64_W4M2_K2};
     static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
                                 TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8, TILE_RING_DEFAULT,
-                                TILE_RING_FIRST + 12, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};
+                                TILE_RING_HALF, TILE_RING_FIRST + 12, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};
     const int *cands = dtype == PT_FLOAT32 ? kFp32 : kHalf;
     const int ncand = dtype == PT_FLOAT32 ? (int)(sizeof(kFp32) / sizeof(int)) : (int)(sizeof(kHalf) / sizeof(int));
     hipStream_t s = stream_of(stream);

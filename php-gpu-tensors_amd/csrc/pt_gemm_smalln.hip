@@ -106,8 +106,12 @@ bool gemm_smalln_eligible(const GemmArgs &g)
 {
     // m-contiguous A (a transposed operand) keeps the MFMA split-K path: a
     // streaming kernel for it measured no faster (27.9 us against 26.9 us on
-    // [1024 x 4096] x [4096 x 10])
-    return g.N <= 16 && g.a_sk == 1 && (double)g.M * g.K >= (double)(1 << 18);
+    // [1024 x 4096] x [4096 x 10]).  The kernel has no K split, so it also
+    // needs one 16-row block per CU at least: a short, long-K product (16 x
+    // 65536, 64 x 4096) would stream all of A through a few workgroups,
+    // where the split-K path spreads K over about 512.
+    return g.N <= 16 && g.a_sk == 1 && (double)g.M * g.K >= (double)(1 << 18) &&
+           (long long)((g.M + 15) / 16) * g.batch >= 256;
 }
 
 void launch_gemm_smalln(const GemmArgs &g, hipStream_t s)

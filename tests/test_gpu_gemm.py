@@ -68,6 +68,12 @@ SHAPES = [(1, 64, 64, 64), (2, 256, 128, 64), (3, 100, 70, 33), (1, 512, 256, 51
           (1, 196, 100, 64), (2, 132, 260, 128)]
 
 
+def smalln_expected(b_, m, n, k):
+    """The small-N kernel's eligibility (pt_gemm_smalln.hip): N <= 16,
+    k-contiguous A, M*K >= 2^18 and one 16-row block per CU (256)."""
+    return n <= 16 and m * k >= 1 << 18 and ((m + 15) // 16) * b_ >= 256
+
+
 def _ints(shape, seed, lo=-8, hi=8):
     from phptensors import synthetic
     return synthetic.integers(shape, lo, hi, seed=seed).astype(np.float32)
@@ -129,7 +135,7 @@ def test_matmul_split_k(A, bmnk, dt):
     b = O.to_storage(_ints((b_, k, n), seed=k + 4, lo=-3, hi=3), dt)
     assert np.array_equal(run(A, a, b, dt), ref(a, b, dt))
     path = A.backend_info().last_matmul.decode()
-    if dt == O.F32 and n <= 16 and m * k >= 1 << 18:
+    if dt == O.F32 and smalln_expected(b_, m, n, k):
         assert path == "mfma-fp32-smalln"   # the streaming small-N kernel
     else:
         assert path.endswith("splitk")
@@ -175,14 +181,14 @@ def test_matmul_direct_lds_kernel(A, dt, layout, bmnk):
         A.load().pt_matmul_set_tile(-1)
 
 
-@pytest.mark.parametrize("tile", list(range(14, 32)))
+@pytest.mark.parametrize("tile", list(range(14, 38)))
 @pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "NT"])
 @pytest.mark.parametrize("bmnk", [(2, 512, 256, 512), (1, 256, 512, 384), (3, 256, 256, 128),
                                   (1, 256, 256, 96), (1, 512, 384, 256)], ids=str)
 def test_matmul_ring_kernel(A, tile, dt, layout, bmnk):
-    """Tiles 14-31 (k_gemm_ring: K step x stages x tile width x schedule x
-    waves):
+    """Tiles 14-37 (k_gemm_ring: K step x stages x tile width x schedule x
+    waves; 32-36: the ping-pong kernel k_gemm_pp; 37: k_gemm_wl):
     exact on integer-valued operands for row-major and k-contiguous B,
     including K-step counts that are not a multiple of the stage count
     (384 / 32 = 12 steps on the 5-stage ring, 128 / 32 = 4 < 5 steps) and
@@ -206,15 +212,18 @@ def test_matmul_ring_kernel(A, tile, dt, layout, bmnk):
 
 @pytest.mark.parametrize("layout", ["NN", "TN", "NT"])
 @pytest.mark.parametrize("bmnk", [(1, 4096, 10, 1024), (1, 1024, 10, 4096), (2, 333, 7, 2500),
-                                  (1, 100, 16, 3000), (3, 517, 1, 700), (1, 64, 8, 4096)], ids=str)
+                                  (16, 333, 7, 2500), (1, 100, 16, 3000), (40, 100, 16, 3000),
+                                  (3, 517, 1, 700), (8, 517, 1, 700), (1, 64, 8, 4096), (64, 64, 8, 4096),
+                                  (1, 16, 10, 65536)], ids=str)
 def test_matmul_smalln(A, bmnk, layout):
     """fp32 products with N <= 16 and k-contiguous A run the small-N kernel
     (pt_gemm_smalln.hip: eight waves over interleaved 16-k groups, B in LDS
-    chunks of 1024 k rows, so K = 2500, 3000 and 4096 run several chunks);
-    a transposed A (TN) keeps the MFMA tiles.  Integer inputs: bit-exact;
-    random inputs: the fp32 bar of the module docstring.  Ragged M (333,
-    517, 100) and N = 1, 7, 8, 10, 16 cover the column padding and the
-    clamped rows."""
+    chunks of 1024 k rows, so K = 2500, 3000 and 4096 run several chunks)
+    when they have a 16-row block per CU; a transposed A (TN) and the short,
+    long-K shapes (1024 x 4096, 64 x 4096, 16 x 65536 in one batch) keep the
+    MFMA split-K path.  Integer inputs: bit-exact; random inputs: the fp32
+    bar of the module docstring.  Ragged M (333, 517, 100) and N = 1, 7, 8,
+    10, 16 cover the column padding and the clamped rows."""
     from phptensors import synthetic
     b_, m, n, k = bmnk
     for trial in ("ints", "normal"):
@@ -235,7 +244,7 @@ def test_matmul_smalln(A, bmnk, layout):
             kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
         got = run(A, a_in, b_in, O.F32, **kw)
         path = A.backend_info().last_matmul.decode()
-        if layout == "TN":
+        if layout == "TN" or not smalln_expected(b_, m, n, k):
             assert path.startswith("mfma-fp32") and "smalln" not in path
         else:
             assert path == "mfma-fp32-smalln"
@@ -426,6 +435,23 @@ def test_config4_full_size_every_output(A, dt):
     worst = float(np.max(err / bound))
     assert np.isfinite(got).all()
     assert bad == 0, f"{bad} outputs outside tolerance (worst {worst:.3g} of the bound)"
+
+
+def test_config1_on_the_gpu(A):
+    """Config 1 (A[256,512] @ B[512,256] fp32 U(-1,1) from seed S1 = 1, the
+    HostArray product of contiguous_array_ce.c:1295-1343) through the HIP
+    fp32 GEMM, element-wise against the oracle's sequential-fmaf product
+    within the north-star GEMM bar 1e-4 * sqrt(K) * (|A||B|)_ij, and within
+    gamma_K of the float64 product."""
+    a, b = O.config1_operands()
+    got = run(A, a, b, O.F32).astype(np.float64)
+    expect = ref(a, b, O.F32).astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    assert got.shape == (256, 256)
+    assert np.all(np.abs(got - expect) <= 1e-4 * math.sqrt(512) * scale)
+    exact = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 512 * 2.0 ** -24 * scale)
+    assert A.backend_info().last_matmul.decode().startswith("mfma-fp32")
 
 
 # ------------------------------------------------ precision policy and tuning
