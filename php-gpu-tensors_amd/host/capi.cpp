@@ -81,6 +81,7 @@ void phpt_strides(phpt_tensor *t, size_t *strides)
 size_t phpt_size(phpt_tensor *t) { return t->t->numel(); }
 int phpt_is_lazy(phpt_tensor *t) { return t->t->lazy() ? 1 : 0; }
 int phpt_is_view(phpt_tensor *t) { return t->t->is_view ? 1 : 0; }
+const void *phpt_device_pointer(phpt_tensor *t) { return t->t->lazy() ? nullptr : t->t->data(); }
 int phpt_dtype_from_name(const char *name) { return dtype_from_name(name); }
 const char *phpt_dtype_name(int dtype) { return dtype_name(dtype); }
 

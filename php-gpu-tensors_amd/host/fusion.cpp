@@ -1286,9 +1286,11 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         const int kind = p->items[st.item].t->node->native.kind;
         if (kind == NAT_GATHER || kind == NAT_SCATTER_ADD) p->indexed = true;
     }
+    // (fusion_plan.c:505-509: an indexed step makes the plan neither stream-
+    // nor graph-compatible, with the incompatibility "indexed-operation")
     if (p->indexed) {
         p->graph_compatible = false;
-        p->incompatibility = "indexed native steps validate their indices on the host";
+        p->incompatibility = "indexed-operation";
     }
     return p;
 }
@@ -1739,7 +1741,9 @@ static bool execute(Plan &p, const std::vector<TensorP> &inputs, std::vector<Ten
         if (!ran && copies == kReplayCopies && !native_present) {
             if ((!p.batch_graph || p.batch_ptrs != p.graph_ptrs) && !capture_copies(p, vals, copies)) return false;
             if (!check_status(pt_graph_launch(p.batch_graph, nullptr), "Graph launch failed")) return false;
-            p.graph_launches += copies;
+            // graphLaunches counts hipGraphLaunch calls (one per cuGraphLaunch in
+            // fusion_execute.c:588-595), executions count executions
+            p.graph_launches++;
             p.executions += copies - 1;
             if (ran_copies) *ran_copies = copies;
         } else if (!ran) {
@@ -1993,7 +1997,8 @@ int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor
     return (int)outs.size();
 }
 
-int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count)
+int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count, phpt_tensor **outputs,
+                      int noutputs)
 {
     clear_error();
     Plan &p = *g->plan;
@@ -2007,19 +2012,21 @@ int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int coun
     }
     std::vector<TensorP> ins, outs;
     if (!bind(p, inputs, ninputs, ins)) return -1;
-    // outputs are dropped between replays, so every replay reuses the same
-    // buffers and the captured graph; whole groups of kReplayCopies go
-    // through one graph launch; one synchronization at the end
+    // each execution's outputs are dropped before the next one, so every
+    // replay reuses the same buffers and the captured graph; whole groups of
+    // kReplayCopies go through one graph launch; one synchronization at the
+    // end, after which the last execution's outputs are handed back
     for (int i = 0; i < count;) {
         int ran = 1;
         const int n = count - i >= kReplayCopies ? kReplayCopies : 1;
-        if (!execute(p, ins, outs, false, n, &ran)) return -1;
         outs.clear();
+        if (!execute(p, ins, outs, false, n, &ran)) return -1;
         i += ran;
     }
     if (!check_status(pt_stream_synchronize(nullptr), "Fusion synchronization failed")) return -1;
     p.synchronizations++;
-    return 0;
+    for (int i = 0; i < noutputs && i < (int)outs.size(); i++) outputs[i] = wrap(outs[i]);
+    return (int)outs.size();
 }
 
 // FusionExecution (fusion.c:561-692): each submitted run owns its outputs,
@@ -2037,8 +2044,8 @@ phpt_execution *phpt_graph_run_async(phpt_graph *g, phpt_tensor **inputs, int ni
 {
     clear_error();
     Plan &p = *g->plan;
-    if (p.indexed) {
-        set_runtime("FusionGraph::runAsync is not available for plans with indexed operations");
+    if (p.indexed) {  // fusion.c:565-569
+        set_runtime("runAsync requires a stream-compatible plan: %s", p.incompatibility);
         return nullptr;
     }
     std::vector<TensorP> ins, outs;
@@ -2119,8 +2126,14 @@ const char *phpt_graph_stats(phpt_graph *g)
     os << "nodes=" << p.items.size() << ";fusedKernels=" << p.kernels.size() << ";boundaries=" << boundaries
        << ";viewAliases=" << aliases << ";executions=" << p.executions << ";executionSteps=" << p.steps.size() + aliases
        << ";intermediateBuffers=" << intermediates << ";cacheHit=" << (p.cache_hit ? 1 : 0)
-       << ";backend=" << (p.use_graph ? "cuda-graph" : "stream")
+       // fusion.c:747-748: a graph only when requested and compatible, else
+       // "stream" for stream-compatible plans and "native" for the others
+       << ";backend=" << (p.use_graph && p.graph_compatible ? "cuda-graph" : p.indexed ? "native" : "stream")
        << ";asyncCompatible=" << (p.indexed ? 0 : 1) << ";cudaGraphCompatible=" << (p.graph_compatible ? 1 : 0)
+       // fusion.c:750-754
+       << ";cudaGraphIncompatibility="
+       << (p.graph_compatible ? "null" : p.incompatibility ? p.incompatibility : "native-graph-not-supported")
+       << ";incompatibility=" << (p.incompatibility ? p.incompatibility : "null")
        << ";graphReplay=" << (p.use_graph && !native_present ? 1 : 0)
        << ";graphLaunches=" << p.graph_launches << ";bufferReuses=" << p.buffer_reuses
        << ";pending=" << p.pending << ";cudaGraphRequested=" << (p.use_graph ? 1 : 0)

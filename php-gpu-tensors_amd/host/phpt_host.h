@@ -44,6 +44,11 @@ int phpt_is_lazy(phpt_tensor *t);
 /* 1 for a tensor made by a view operation (slice, transpose, reshape,
  * broadcast, select): __serialize refuses those (cuda_array_ce.c:276-280) */
 int phpt_is_view(phpt_tensor *t);
+/* Device address of the tensor's first element (storage plus offset), for
+ * a host that hands the buffer to another library; NULL for a value still
+ * recorded in a Fusion scope.  No counterpart in the reference, whose
+ * tensor_t exposes its pointer to C code directly (src/tensor.h:49-79). */
+const void *phpt_device_pointer(phpt_tensor *t);
 int phpt_dtype_from_name(const char *name);
 const char *phpt_dtype_name(int dtype);
 
@@ -92,11 +97,15 @@ phpt_graph *phpt_fusion_end(phpt_tensor **outputs, int count, int use_graph);
  * every recorded value still referenced elsewhere) with its result. */
 int phpt_fusion_run_once(phpt_tensor **outputs, int count);
 int phpt_graph_run(phpt_graph *g, phpt_tensor **inputs, int ninputs, phpt_tensor **outputs, int noutputs);
-/* Replays the plan `count` times back to back on the runtime stream and
- * synchronizes once (outputs are discarded).  No counterpart in the
- * reference, whose run() synchronizes per replay (fusion.c:599-641); it
- * exists to time replay throughput. */
-int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count);
+/* Replays the plan `count` times back to back on the runtime stream,
+ * synchronizes once and returns the last execution's outputs (like
+ * phpt_graph_run: their number, or -1).  Each execution drops the one
+ * before it, so all reuse the plan's buffers, and whole groups of eight run
+ * through one graph launch.  No counterpart in the reference, whose run()
+ * synchronizes per replay (fusion.c:599-641); it exists to time replay
+ * throughput. */
+int phpt_graph_replay(phpt_graph *g, phpt_tensor **inputs, int ninputs, int count, phpt_tensor **outputs,
+                      int noutputs);
 /* FusionGraph::runAsync / FusionExecution (fusion.c:561-692): each
  * submission returns its own execution (NULL on error); several may be
  * pending for a plan without a captured graph.  wait returns the number of

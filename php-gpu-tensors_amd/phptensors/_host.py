@@ -59,7 +59,9 @@ SIGNATURES = {
     "phpt_fusion_end": (G, [ctypes.POINTER(T), ctypes.c_int, ctypes.c_int]),
     "phpt_fusion_run_once": (ctypes.c_int, [ctypes.POINTER(T), ctypes.c_int]),
     "phpt_graph_run": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.POINTER(T), ctypes.c_int]),
-    "phpt_graph_replay": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.c_int]),
+    "phpt_graph_replay": (ctypes.c_int, [G, ctypes.POINTER(T), ctypes.c_int, ctypes.c_int, ctypes.POINTER(T),
+                                         ctypes.c_int]),
+    "phpt_device_pointer": (ctypes.c_void_p, [T]),
     "phpt_graph_run_async": (ctypes.c_void_p, [G, ctypes.POINTER(T), ctypes.c_int]),
     "phpt_execution_wait": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(T), ctypes.c_int]),
     "phpt_execution_is_finished": (ctypes.c_int, [ctypes.c_void_p]),
@@ -115,6 +117,9 @@ def parse_kv(text):
         if not part:
             continue
         k, _, v = part.partition("=")
+        if v == "null":
+            out[k] = None
+            continue
         try:
             out[k] = int(v)
         except ValueError:

@@ -156,10 +156,16 @@ class FusionGraph:
         return self._rebuild([CudaArray._wrap(outs[i]) for i in range(n)])
 
     def replay(self, count, *inputs):
-        """Replay `count` times back to back and synchronize once, discarding
-        the outputs (throughput measurement; not part of the reference API)."""
-        if _host.load().phpt_graph_replay(self._g, _handles(inputs), len(inputs), int(count)) != 0:
+        """Replay `count` times back to back, synchronize once and return the
+        last execution's outputs as run() does (throughput measurement; not
+        part of the reference API).  Each execution drops the one before it,
+        so all reuse the plan's buffers."""
+        lib = _host.load()
+        n = lib.phpt_graph_num_outputs(self._g)
+        outs = self._outputs(n)
+        if lib.phpt_graph_replay(self._g, _handles(inputs), len(inputs), int(count), outs, n) < 0:
             _host.raise_error("FusionGraph::replay")
+        return self._rebuild([CudaArray._wrap(outs[i]) for i in range(n)])
 
     def runAsync(self, *inputs):
         self._check_tracking(inputs)

@@ -130,27 +130,11 @@ def test_tanh_x_plus_y_z_vs_oracle():
     assert d.max() <= 4
 
 
-def test_config3_full_size_replay_vs_oracle():
-    """The plan bench.py times (config 3), at its full size and seeds: x, z
-    [16384, 8192] U(-2, 2) (seeds 3, 31), y [8192] (seed 32), compiled with
-    cudaGraph=True and replayed from its HIP graph, as FusionGraph::run
-    replays it (fusion_execute.c:385-598).  Every output element (all 134 M,
-    in chunks of 2048 rows) is checked against the oracle's per-op
-    composition: y*z and x+m rounded per op (exact), tanh within 4 ulp of
-    libm, so every workgroup of the grid and the kernel's index decode up to
-    its last element are covered."""
-    from phptensors import synthetic
-    rows, n = 16384, 8192
-    xs = synthetic.uniform((rows, n), -2.0, 2.0, seed=3)
-    zs = synthetic.uniform((rows, n), -2.0, 2.0, seed=31)
-    ys = synthetic.uniform((n,), -2.0, 2.0, seed=32)
-    x, y, z = (CudaArray.fromNumpy(v) for v in (xs, ys, zs))
-    graph = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z], cudaGraph=True)
-    graph.replay(3, x, y, z)
-    out = graph.run(x, y, z)
-    assert [s["kind"] for s in graph.getPlan()] == ["fused"]
-    assert graph.getStats()["graphLaunches"] >= 2
-    got_all = out.toNumpy()
+def _config3_oracle_check(xs, ys, zs, got_all):
+    """Every output element against the oracle's per-op composition, in
+    chunks of 2048 rows: y*z and x+m rounded per op (exact), tanh within
+    4 ulp of libm."""
+    rows = xs.shape[0]
     for r0 in range(0, rows, 2048):
         got = got_all[r0:r0 + 2048]
         mul = O.binary(ys, O.F32, zs[r0:r0 + 2048], O.F32, "mul", O.F32)
@@ -158,6 +142,53 @@ def test_config3_full_size_replay_vs_oracle():
         ref = O.unary(add, O.F32, "tanh")
         d = np.abs(got.view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
         assert d.max() <= 4, (r0, int(d.max()), np.unravel_index(int(d.argmax()), d.shape))
+
+
+def test_config3_full_size_replay_vs_oracle():
+    """The path bench.py times (config 3) at its full size and seeds: x, z
+    [16384, 8192] U(-2, 2) (seeds 3, 31), y [8192] (seed 32), compiled with
+    cudaGraph=True.  FusionGraph.replay(16) runs two groups of eight
+    executions, each group one launch of the graph that holds eight copies
+    of the plan.  The plan's output buffer is first filled with NaN bits, so
+    only what the eight-copy graph writes can pass; replay hands back the
+    16th execution's outputs, which must live in that same buffer.  Every
+    output element (all 134 M) is then checked against the oracle.  The
+    stats count each graph launch once (fusion_execute.c:588-595) and each
+    execution once.  run() as the reference calls it (fusion.c:599-641, one
+    single-copy graph launch) is checked the same way."""
+    from phptensors import _abi, _host, synthetic
+    rows, n = 16384, 8192
+    xs = synthetic.uniform((rows, n), -2.0, 2.0, seed=3)
+    zs = synthetic.uniform((rows, n), -2.0, 2.0, seed=31)
+    ys = synthetic.uniform((n,), -2.0, 2.0, seed=32)
+    x, y, z = (CudaArray.fromNumpy(v) for v in (xs, ys, zs))
+    graph = Fusion.compile(lambda a, b, c: (a + b * c).tanh(), [x, y, z], cudaGraph=True)
+    assert [s["kind"] for s in graph.getPlan()] == ["fused"]
+    lib, host = _abi.load(), _host.load()
+    first = graph.run(x, y, z)
+    ptr = host.phpt_device_pointer(first._h)
+    assert ptr
+    _abi.check(lib.pt_memset(ptr, 0xFF, rows * n * 4, None), "poison")
+    _abi.check(lib.pt_device_synchronize(), "synchronize")
+    del first
+    st0 = graph.getStats()
+    out = graph.replay(16, x, y, z)
+    st1 = graph.getStats()
+    assert host.phpt_device_pointer(out._h) == ptr
+    assert st1["graphLaunches"] - st0["graphLaunches"] == 2
+    assert st1["executions"] - st0["executions"] == 16
+    _config3_oracle_check(xs, ys, zs, out.toNumpy())
+    del out
+    # fewer than eight executions: one single-copy graph launch each
+    st0 = graph.getStats()
+    graph.replay(3, x, y, z)
+    st1 = graph.getStats()
+    assert st1["graphLaunches"] - st0["graphLaunches"] == 3
+    assert st1["executions"] - st0["executions"] == 3
+    _abi.check(lib.pt_memset(ptr, 0xFF, rows * n * 4, None), "poison")
+    out = graph.run(x, y, z)
+    assert host.phpt_device_pointer(out._h) == ptr
+    _config3_oracle_check(xs, ys, zs, out.toNumpy())
 
 
 def test_plan_natives_vs_oracle():
@@ -426,10 +457,12 @@ def test_native_plan_with_workspace_replays_from_graph():
 def test_replay_groups_of_copies_keep_results_and_stats(count):
     """FusionGraph::replay launches whole groups of eight executions of a
     plan without native steps as one graph that holds eight copies of its
-    steps (here three kernels on parallel branches).  Every execution is
-    counted as a graph launch, a run after the replays gives the eager
-    results bit for bit, and replays with another input buffer capture both
-    graphs again, so that later runs follow the new input."""
+    steps (here three kernels on parallel branches).  graphLaunches counts
+    each hipGraphLaunch once (a group of eight is one), executions count
+    every execution; the outputs replay hands back (the last execution's)
+    and a run after the replays give the eager results bit for bit, and
+    replays with another input buffer capture both graphs again, so that
+    later runs follow the new input."""
     r = np.random.default_rng(90 + count)
     x = CudaArray.fromNumpy(r.standard_normal((1000, 33)).astype(np.float32))
     y = CudaArray.fromNumpy(r.standard_normal((33,)).astype(np.float32))
@@ -440,11 +473,15 @@ def test_replay_groups_of_copies_keep_results_and_stats(count):
 
     graph = Fusion.compile(body, [x, y, z], cudaGraph=True)
     assert len(graph.getPlan()) >= 2
+    launches = count // 8 + count % 8
     st0 = graph.getStats()
-    graph.replay(count, x, y, z)
+    last = graph.replay(count, x, y, z)
     st1 = graph.getStats()
-    assert st1["graphLaunches"] - st0["graphLaunches"] == count
+    assert st1["graphLaunches"] - st0["graphLaunches"] == launches
     assert st1["executions"] - st0["executions"] == count
+    for i, (o, e) in enumerate(zip(last, body(x, y, z))):
+        assert np.array_equal(o.toBits(), e.toBits()), ("replay", i)
+    del last
     for rep in range(2):
         for i, (o, e) in enumerate(zip(graph.run(x, y, z), body(x, y, z))):
             assert np.array_equal(o.toBits(), e.toBits()), (rep, i)
@@ -453,7 +490,7 @@ def test_replay_groups_of_copies_keep_results_and_stats(count):
     graph.replay(count, x2, y, z)
     for i, (o, e) in enumerate(zip(graph.run(x2, y, z), body(x2, y, z))):
         assert np.array_equal(o.toBits(), e.toBits()), i
-    assert graph.getStats()["graphLaunches"] - st1["graphLaunches"] == count + 3  # and three runs
+    assert graph.getStats()["graphLaunches"] - st1["graphLaunches"] == launches + 3  # and three runs
 
 
 # ------------------------------------------- dependent outputs (reference)

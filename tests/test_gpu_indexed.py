@@ -117,6 +117,17 @@ def test_reference_fusion_plans():
     assert gather_graph.getStats()["asyncCompatible"] in (0, False)
     assert not gather_graph.getStats()["cudaGraphCompatible"]
     assert not scatter_graph.getStats()["cudaGraphCompatible"]
+    # fusion_plan.c:505-509 and fusion.c:747-754: an indexed plan is neither
+    # stream- nor graph-compatible, so it reports the "native" backend, also
+    # when a graph was requested
+    for st in (gather_graph.getStats(), scatter_graph.getStats()):
+        assert st["backend"] == "native"
+        assert st["incompatibility"] == "indexed-operation"
+        assert st["cudaGraphIncompatibility"] == "indexed-operation"
+    requested = Fusion.compile(lambda x, i: x.gather(i, 1), [source, indices], cudaGraph=True)
+    assert requested.run(source, indices).toArray() == [[30.0, 10.0], [50.0, 50.0]]
+    assert requested.getStats()["backend"] == "native"
+    assert requested.getStats()["cudaGraphRequested"] == 1
     transposed = source.transpose()
     tidx = idx_array([2, 0, 1, 2, 0, 1], [3, 2])
     tgraph = Fusion.compile(lambda x, i: x.gather(i, 0), [transposed, tidx])
@@ -133,9 +144,10 @@ def test_reference_fusion_plans():
     with pytest.raises(InvalidArgumentException, match=r"scatterAdd indices must be within \[0, 3\)"):
         scatter_graph.run(base, bad, updates)
     assert scatter_graph.run(base, indices, updates).toArray() == [[2.0, 0.0, 1.0], [0.0, 7.0, 0.0]]
-    with pytest.raises(RuntimeException):
+    # fusion.c:565-569
+    with pytest.raises(RuntimeException, match="runAsync requires a stream-compatible plan: indexed-operation"):
         gather_graph.runAsync(source, indices)
-    with pytest.raises(RuntimeException):
+    with pytest.raises(RuntimeException, match="runAsync requires a stream-compatible plan: indexed-operation"):
         scatter_graph.runAsync(base, indices, updates)
 
 
