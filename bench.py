@@ -53,8 +53,8 @@ PMC_TRAFFIC_BYTES = {
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol
-GEMM_KERNELS = {"mfma-lds-ring": "k_gemm_ring", "mfma-direct-lds": "k_gemm_direct", "mfma-fp32": "k_gemm",
-                "mfma-low-precision": "k_gemm"}
+GEMM_KERNELS = {"mfma-lds-wholeline": "k_gemm_wl", "mfma-lds-pingpong": "k_gemm_pp", "mfma-lds-ring": "k_gemm_ring",
+                "mfma-direct-lds": "k_gemm_direct", "mfma-fp32": "k_gemm", "mfma-low-precision": "k_gemm"}
 MALL_BYTES = 256 << 20
 
 
@@ -236,7 +236,7 @@ def fused_family(steps, warmup, replays=100):
                         "y [8192] seed 32; compiled once, replayed 100x via hipGraph",
             "ms_per_step": ms * replays, "GB/s": gbs, "frac": gbs / HBM_PEAK_GBS,
             "ops": {"tanh_x_plus_y_z": res}, "plan": plan,
-            "stats": {k: stats[k] for k in ("fusedKernels", "graphLaunches", "cudaGraphCompatible")}}
+            "stats": {k: stats[k] for k in ("fusedKernels", "graphLaunches", "executions", "cudaGraphCompatible")}}
 
 
 def eager_family(steps, warmup):
@@ -753,9 +753,13 @@ def main():
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp32", "data": "synthetic (SplitMix64/Box-Muller, fixed seeds)",
-        "config": {"workload": "; ".join(fams[f]["workload"] for f in ("reduce", "fused", "gemm") if f in fams),
-                   "families": sorted(fams)},
+        # the reduce and fused families compute in fp32, the GEMM headline in
+        # bf16 with fp32 accumulation (fp16 and fp32 GEMMs reported beside it)
+        "dtype": "fp32+bf16", "data": "synthetic (SplitMix64/Box-Muller, fixed seeds)",
+        "config": {"workload": "configs 2-4: fp32 row reductions X[8192,4096]; Fusion tanh(x+y*z) [16384,8192] x100 "
+                               "hipGraph replays; batched GEMM [32,2048,2048]^2 bf16 (fp16, fp32 beside)",
+                   "families": sorted(fams),
+                   "details": {f: fams[f]["workload"] for f in ("reduce", "fused", "gemm") if f in fams}},
         "families": {k: {kk: vv for kk, vv in v.items()} for k, v in fams.items()},
         "roofline": roofline,
         # the north-star kernel (bf16 batched GEMM) against the dense bf16 MFMA peak

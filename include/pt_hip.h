@@ -187,8 +187,13 @@ int pt_reduce_result_dtype(int dtype, int op);
  * column-split partials, the packed copy of a strided input) comes from a
  * static 1 MiB buffer the library holds on each device, not from the pool;
  * nothing is allocated.  A reduction that needs more scratch fails with
- * PT_ERR_INVALID.  Every call on a device shares that device's buffer:
- * calls that overlap on one device (other threads or streams) race. */
+ * PT_ERR_INVALID.  Every call on a device shares that device's buffer, and
+ * calls that overlap on one device (other threads or streams) are ordered
+ * on the GPU rather than racing: each call's stream waits for the event the
+ * previous call recorded after its kernels (created once per device at the
+ * first call; a call allocates nothing).  Under stream capture that
+ * hand-off is skipped, so a graph holding the call must not run while
+ * another call on the device does. */
 pt_status pt_reduce_noalloc(const void *input, void *output, int dtype, int op,
                             const int *shape, const size_t *strides, int ndims, int axis,
                             size_t base_offset, pt_stream_t stream);

@@ -21,10 +21,12 @@ hipStream_t stream_of(pt_stream_t s);
 pt_status ensure_init();
 pt_status scratch_alloc(void **ptr, size_t bytes, hipStream_t stream);
 void scratch_free(void *ptr, hipStream_t stream);
-// static scratch of the no-allocation entry points (1 MiB per device)
+// static scratch of the no-allocation entry points (1 MiB per device);
+// begin orders the call's stream after the previous call's work on the
+// device, end records the call's own (both on `stream`)
 #define PT_STATIC_SCRATCH_BYTES (1u << 20)
-pt_status static_scratch_begin();
-void static_scratch_end();
+pt_status static_scratch_begin(hipStream_t stream);
+pt_status static_scratch_end(hipStream_t stream);
 pt_backend_info &counters();
 
 #define PT_TRY(expr)                      \

@@ -130,9 +130,12 @@ __device__ __forceinline__ double exp_c(double a) { return exp(a); }
 // a / b for many a and one b.  fp32: with rb = RN(1 / b) (one true division
 // per row), q0 = RN(a rb) is within one ulp of a / b and the fma remainder
 // a - b q0 is exact, so RN(q0 + (a - b q0) rb) is the correctly rounded
-// quotient (Markstein's theorem; outside the subnormal range, where it
-// stays within one ulp): three instructions instead of the ~10 of an IEEE
-// division.  Callers take the true division when rb is 0 or not finite.
+// quotient (Markstein's theorem): three instructions instead of the ~10 of
+// an IEEE division.  The theorem needs a normal quotient, so a quotient at
+// or below FLT_MIN (a softmax value more than about 87 below its row's
+// maximum) takes the IEEE division; the branch is uniform and skipped
+// unless a lane needs it.  Callers take the true division when rb is 0 or
+// not finite.
 struct RowDiv {
     float b, rb;
     bool fast;
@@ -143,6 +146,7 @@ struct RowDiv {
     __device__ __forceinline__ float operator()(float a) const
     {
         const float q0 = a * rb;
+        if (__builtin_expect(__builtin_fabsf(q0) <= 1.17549435e-38f, 0)) return a / b;
         return __builtin_fmaf(__builtin_fmaf(-q0, b, a), rb, q0);
     }
 };
@@ -1830,11 +1834,12 @@ pt_status pt_reduce_noalloc(const void *input, void *output, int dtype, int op,
     if (rop < 0 || rop == R_ARGMAX || rop == R_ARGMIN)
         return fail(PT_ERR_INVALID, "pt_reduce_noalloc: unsupported op %d", op);
     PT_TRY(ensure_init());
-    PT_TRY(static_scratch_begin());
+    hipStream_t s = stream_of(stream);
+    PT_TRY(static_scratch_begin(s));
     pt_status st = reduce_driver(input, output, dtype, rop, result_dtype(dtype, rop), shape, strides, ndims,
-                                 axis, base_offset, 0, 0, stream);
-    static_scratch_end();
-    return st;
+                                 axis, base_offset, 0, 0, s);
+    const pt_status end = static_scratch_end(s);
+    return st != PT_OK ? st : end;
 }
 
 pt_status pt_arg_reduce(const void *input, int32_t *output, int dtype, int op,

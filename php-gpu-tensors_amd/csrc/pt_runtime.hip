@@ -108,11 +108,27 @@ hipStream_t stream_of(pt_stream_t s)
 // address: its device address is looked up per device with
 // hipGetSymbolAddress (with that device current) the first time an entry
 // point runs there.
+//
+// Calls that overlap on one device (other threads, other streams) are
+// ordered on the GPU instead of racing on the array: each device keeps the
+// event the last call recorded on its stream after its kernels, and a call
+// makes its own stream wait for that event before its first kernel.  The
+// wait, the kernels and the record happen under one host lock, so the
+// hand-off order is the order in which the calls take the lock.  The event
+// is created with the device's address, once, at the first call there; a
+// call allocates nothing.  Under stream capture the hand-off is skipped
+// (the graph orders its own nodes), so a graph holding such a call must not
+// run while another call on that device does.
 static __device__ __align__(256) unsigned char scratch[PT_STATIC_SCRATCH_BYTES];
-static std::mutex g_static_mu;
+static std::mutex g_static_mu;       // set-up of the per-device entries
+static std::mutex g_static_call_mu;  // held from static_scratch_begin to static_scratch_end
 static void *g_static_ptr[64];
+static hipEvent_t g_static_last[64];
+static bool g_static_recorded[64];
+static thread_local int t_static_dev = -1;
+static thread_local bool t_static_capturing = false;
 
-pt_status static_scratch_address(void **ptr)
+static pt_status static_scratch_setup(int *dev_out, void **ptr)
 {
     int dev = 0;
     PT_TRY(check_hip(hipGetDevice(&dev), "hipGetDevice"));
@@ -122,8 +138,11 @@ pt_status static_scratch_address(void **ptr)
         void *p = nullptr;
         PT_TRY(check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "static scratch address"));
         if (!p) return fail(PT_ERR_RUNTIME, "static scratch has no device address");
+        PT_TRY(check_hip(hipEventCreateWithFlags(&g_static_last[dev], hipEventDisableTiming),
+                         "static scratch event"));
         g_static_ptr[dev] = p;
     }
+    *dev_out = dev;
     *ptr = g_static_ptr[dev];
     return PT_OK;
 }
@@ -195,11 +214,24 @@ void scratch_free(void *ptr, hipStream_t stream)
 // Scratch of the calls between static_scratch_begin and static_scratch_end
 // comes from the device's static scratch array (a stack, as a workspace);
 // a request beyond it fails with PT_ERR_INVALID instead of allocating.
-pt_status static_scratch_begin()
+pt_status static_scratch_begin(hipStream_t stream)
 {
     if (t_ws.active) return fail(PT_ERR_INVALID, "a workspace is already active on this thread");
     void *p = nullptr;
-    PT_TRY(static_scratch_address(&p));
+    int dev = 0;
+    PT_TRY(static_scratch_setup(&dev, &p));
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    PT_TRY(check_hip(hipStreamIsCapturing(stream, &cap), "hipStreamIsCapturing"));
+    g_static_call_mu.lock();
+    if (cap == hipStreamCaptureStatusNone && g_static_recorded[dev]) {
+        const pt_status st = check_hip(hipStreamWaitEvent(stream, g_static_last[dev], 0), "static scratch hand-off");
+        if (st != PT_OK) {
+            g_static_call_mu.unlock();
+            return st;
+        }
+    }
+    t_static_dev = dev;
+    t_static_capturing = cap != hipStreamCaptureStatusNone;
     t_ws = Workspace();
     t_ws.active = true;
     t_ws.fixed = true;
@@ -208,9 +240,18 @@ pt_status static_scratch_begin()
     return PT_OK;
 }
 
-void static_scratch_end()
+pt_status static_scratch_end(hipStream_t stream)
 {
     t_ws = Workspace();
+    pt_status st = PT_OK;
+    const int dev = t_static_dev;
+    if (!t_static_capturing) {
+        st = check_hip(hipEventRecord(g_static_last[dev], stream), "static scratch hand-off record");
+        if (st == PT_OK) g_static_recorded[dev] = true;
+    }
+    t_static_dev = -1;
+    g_static_call_mu.unlock();
+    return st;
 }
 
 }  // namespace pt

@@ -319,3 +319,12 @@ def scatter_add(x, dtype, indices, updates, axis):
     if st != 0:
         raise OracleIndexError(bad.value)
     return out
+
+
+def config1_operands():
+    """A[256,512] and B[512,256] fp32 U(-1,1)
+    from seed S1 = 1 of the SplitMix64 generator (phptensors/synthetic.py):
+    one stream of 2 * 131072 values, A first, then B."""
+    from phptensors import synthetic
+    ab = synthetic.uniform((2 * 256 * 512,), -1.0, 1.0, seed=1)
+    return ab[:256 * 512].reshape(256, 512).copy(), ab[256 * 512:].reshape(512, 256).copy()

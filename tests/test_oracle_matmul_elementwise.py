@@ -51,12 +51,23 @@ def test_matmul_integer_valued_exact_and_error_bound():
     b = rng.integers(-8, 8, size=(3, 70, 21)).astype(np.float32)
     c = O.matmul(a, b, O.F32)
     assert np.array_equal(c.astype(np.float64), a.astype(np.float64) @ b.astype(np.float64))
-    a = rng.uniform(-1, 1, size=(256, 512)).astype(np.float32)
-    b = rng.uniform(-1, 1, size=(512, 256)).astype(np.float32)
+    # config 1 (A[256,512] @ B[512,256], U(-1,1) from seed S1 = 1 of the
+    # bench's SplitMix64 generator): within gamma_K of the float64 product
+    a, b = O.config1_operands()
     c = O.matmul(a, b, O.F32).astype(np.float64)
     ref = a.astype(np.float64) @ b.astype(np.float64)
     scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
     assert np.all(np.abs(c - ref) <= 512 * 2.0 ** -24 * scale)
+    # the sequential fmaf order of contiguous_array_ce.c:1327-1333 (one
+    # rounding per step of the exact a*b + acc), in exact rational
+    # arithmetic for a sample of outputs
+    from fractions import Fraction
+    from test_rowdiv_rounding import rn32
+    for i, j in ((0, 0), (17, 200), (255, 255), (128, 3)):
+        acc = Fraction(0)
+        for k in range(512):
+            acc = rn32(Fraction(float(a[i, k])) * Fraction(float(b[k, j])) + acc)
+        assert c[i, j] == float(acc), (i, j)
 
 
 def test_matmul_bf16_output_is_rne_of_fp32_product():

@@ -2,19 +2,24 @@
 csrc/pt_reduce.hip): with rb = RN(1/b), q0 = RN(a rb), r = RN(a - b q0)
 (one fma) and q = RN(q0 + r rb) (one fma), q equals the correctly rounded
 fp32 quotient RN(a/b) whenever a, b and a/b are normal (Markstein's
-theorem).  Checked here in exact rational arithmetic, every rounding done
-once and to nearest-even, on the operand ranges the kernels see: softmax
-divides exp values in (0, 1] by a row sum in [1, n], layerNorm divides
-centred values by sqrt(var + eps).  Pure CPU; no GPU code runs."""
+theorem); a quotient with |q0| <= FLT_MIN takes the IEEE division instead.
+Checked here in exact rational arithmetic, every rounding done once and to
+nearest-even on the binary32 grid (subnormals included), on the operand
+ranges the kernels see: softmax divides exp values in (0, 1] by a row sum
+in [1, n], layerNorm divides centred values by sqrt(var + eps), and
+softmax values down to the subnormal range.  Pure CPU; no GPU code runs."""
 from fractions import Fraction
 
 import numpy as np
 import pytest
 
 
+FLT_MIN = Fraction(2) ** -126
+
+
 def rn32(x):
     """Round an exact rational to the nearest binary32 (ties to even),
-    normal range only."""
+    subnormals included (quantum 2^-149 below 2^-126); no overflow."""
     if x == 0:
         return Fraction(0)
     sign = -1 if x < 0 else 1
@@ -23,19 +28,26 @@ def rn32(x):
     if Fraction(2) ** e > x:
         e -= 1
     assert Fraction(2) ** e <= x < Fraction(2) ** (e + 1)
-    assert -126 <= e <= 127, "normal range"
-    m = x / Fraction(2) ** (e - 23)                 # in [2^23, 2^24)
+    assert e <= 127, "no overflow"
+    e = max(e, -126)                                # subnormal: fixed quantum
+    m = x / Fraction(2) ** (e - 23)
     q, r = divmod(m.numerator, m.denominator)
     if 2 * r > m.denominator or (2 * r == m.denominator and q % 2 == 1):
         q += 1
     return sign * Fraction(q) * Fraction(2) ** (e - 23)
 
 
-def rowdiv(a, b):
+def markstein(a, b):
     rb = rn32(1 / b)
     q0 = rn32(a * rb)
     r = rn32(a - b * q0)
-    return rn32(q0 + r * rb)
+    return q0, rn32(q0 + r * rb)
+
+
+def rowdiv(a, b):
+    """RowDiv::operator(): the IEEE quotient when |q0| <= FLT_MIN."""
+    q0, q = markstein(a, b)
+    return rn32(a / b) if abs(q0) <= FLT_MIN else q
 
 
 def f32(v):
@@ -75,3 +87,26 @@ def test_rowdiv_halfway_quotients():
                 for t in (q, q + half, q - half):
                     a = rn32(b * t)
                     assert rowdiv(a, b) == rn32(a / b)
+
+
+def test_rowdiv_subnormal_quotients():
+    """Softmax values whose quotient by the row sum is subnormal or at the
+    normal boundary (exp arguments from about -87 to -104): the guard takes
+    the IEEE division there, so every quotient is correctly rounded; the
+    unguarded three-instruction form is off by an ulp on some of these,
+    which is what the guard is for."""
+    rng = np.random.default_rng(4)
+    off = 0
+    for _ in range(1500):
+        b = f32(rng.uniform(1, 4096))
+        # a / b between 2^-149 and 2^-125
+        a = f32(float(b) * 2.0 ** rng.uniform(-148, -125))
+        if a == 0:
+            continue
+        assert rowdiv(a, b) == rn32(a / b), (float(a), float(b))
+        off += markstein(a, b)[1] != rn32(a / b)
+    assert off > 0
+    # q0 exactly at FLT_MIN: the guard is inclusive
+    b = Fraction(3)
+    a = rn32(FLT_MIN * b)
+    assert rowdiv(a, b) == rn32(a / b)
