@@ -2,6 +2,8 @@
 // Not part of the public boundary (include/pt_hip.h is).
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -177,6 +179,34 @@ __device__ __forceinline__ T wave_reduce(T v, F f)
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v = f(v, __shfl_xor(v, m, PT_WAVE));
     return v;
+}
+
+// Every lane gets the wave's reduction of a 4-byte value, without LDS:
+// two DPP quad permutes (lane ^ 1, lane ^ 2) and the half-row and row
+// mirrors (lane i with 7 - i and 15 - i) combine each 16-lane row, fused
+// into the ALU ops as DPP source modifiers; the four row totals then come
+// out through v_readlane and are combined in one fixed order, so the result
+// is the same wave-uniform value in every lane.  f must be commutative and
+// associative up to the rounding a reduction order may change (add, max,
+// min).
+template <typename T, typename F>
+__device__ __forceinline__ T wave_all(T v, F f)
+{
+    static_assert(sizeof(T) == 4, "4-byte lanes");
+    auto dpp = [](T x, auto CTRL) {
+        return __builtin_bit_cast(
+            T, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), decltype(CTRL)::value, 0xF, 0xF, false));
+    };
+    v = f(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1, 0, 3, 2]
+    v = f(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2, 3, 0, 1]
+    v = f(v, dpp(v, std::integral_constant<int, 0x141>{}));  // row_half_mirror
+    v = f(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+    const int iv = __builtin_bit_cast(int, v);
+    const T a = __builtin_bit_cast(T, __builtin_amdgcn_readlane(iv, 0));
+    const T b = __builtin_bit_cast(T, __builtin_amdgcn_readlane(iv, 16));
+    const T c = __builtin_bit_cast(T, __builtin_amdgcn_readlane(iv, 32));
+    const T d = __builtin_bit_cast(T, __builtin_amdgcn_readlane(iv, 48));
+    return f(f(a, b), f(c, d));
 }
 
 struct FAdd { template <typename T> __device__ T operator()(T a, T b) const { return a + b; } };

@@ -83,8 +83,12 @@ __device__ __forceinline__ void store16(void *dst, const void *src)
 template <typename C, int WPR>
 __device__ __forceinline__ C row_sum(C v, C *lds)
 {
+    if constexpr (sizeof(C) == 4) {
+        v = wave_all(v, FAdd{});
+    } else {
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, PT_WAVE);
+        for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m, PT_WAVE);
+    }
     if constexpr (WPR > 1) {
         const int wave = threadIdx.x >> 6, w0 = wave - wave % WPR;
         __syncthreads();
@@ -101,8 +105,12 @@ template <typename C> __device__ __forceinline__ C fmax_any(C a, C b);
 template <typename C, int WPR>
 __device__ __forceinline__ C row_max(C v, C *lds)
 {
+    if constexpr (sizeof(C) == 4) {
+        v = wave_all(v, [](C a, C b) { return fmax_any(a, b); });
+    } else {
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmax_any(v, __shfl_xor(v, m, PT_WAVE));
+        for (int m = 32; m >= 1; m >>= 1) v = fmax_any(v, __shfl_xor(v, m, PT_WAVE));
+    }
     if constexpr (WPR > 1) {
         const int wave = threadIdx.x >> 6, w0 = wave - wave % WPR;
         __syncthreads();
@@ -252,8 +260,42 @@ template <typename C> struct Acc<C, R_VAR> {
 template <typename C, int OP>
 __device__ __forceinline__ void wave_merge(Acc<C, OP> &a)
 {
+    if constexpr (sizeof(C) == 4 && (OP == R_ARGMAX || OP == R_ARGMIN)) {
+        // (value, index) pairs over the same DPP pattern as wave_all: the
+        // merge keeps the better value and, on ties, the lower index, so it
+        // gives the same pair whichever side a lane holds
+        auto step = [&](auto CTRL) {
+            Acc<C, OP> o;
+            o.v = __builtin_bit_cast(C, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a.v),
+                                                                     decltype(CTRL)::value, 0xF, 0xF, false));
+            o.i = __builtin_amdgcn_update_dpp(0, a.i, decltype(CTRL)::value, 0xF, 0xF, false);
+            a.merge(o);
+        };
+        step(std::integral_constant<int, 0xB1>{});
+        step(std::integral_constant<int, 0x4E>{});
+        step(std::integral_constant<int, 0x141>{});
+        step(std::integral_constant<int, 0x140>{});
+        Acc<C, OP> r[4];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) a.merge_shfl(m);
+        for (int q = 0; q < 4; q++) {
+            r[q].v = __builtin_bit_cast(C, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a.v), 16 * q));
+            r[q].i = __builtin_amdgcn_readlane(a.i, 16 * q);
+        }
+        r[0].merge(r[1]);
+        r[2].merge(r[3]);
+        r[0].merge(r[2]);
+        a = r[0];
+    } else if constexpr (sizeof(C) == 4 && (OP == R_SUM || OP == R_MEAN || OP == R_PROD || OP == R_MAX || OP == R_MIN)) {
+        a.s = wave_all(a.s, [](C x, C y) {
+            if constexpr (OP == R_MAX) return fmax_c(x, y);
+            else if constexpr (OP == R_MIN) return fmin_c(x, y);
+            else if constexpr (OP == R_PROD) return x * y;
+            else return x + y;
+        });
+    } else {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) a.merge_shfl(m);
+    }
 }
 
 // Chunk-level variance update: V elements at once (exact two-pass on the
@@ -306,14 +348,25 @@ template <typename T> struct LdsSlot {
     __align__(16) unsigned char raw[sizeof(T)];
 };
 
+// Block shape of a row kernel with WPR waves per row: WPR = 1 packs four
+// rows into a 256-thread block; WPR >= 4 gives each row a block of WPR
+// waves (64 * WPR threads).
+template <int WPR> struct RowShape {
+    static_assert(WPR == 1 || WPR == 4 || WPR == 8, "waves per row");
+    static constexpr int BW = WPR > 4 ? WPR : 4;  // waves per block
+    static constexpr int RPB = BW / WPR;           // rows per block
+};
+
 template <int DT, int OP, int VEC, int WPR>
-__global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin, size_t rows,
-                                                    int n, size_t ld, void *__restrict__ out,
-                                                    int out_dt, int correction, int take_sqrt)
+__global__ __launch_bounds__(64 * RowShape<WPR>::BW) void k_row_reduce(const void *__restrict__ xin, size_t rows,
+                                                                        int n, size_t ld, void *__restrict__ out,
+                                                                        int out_dt, int correction, int take_sqrt)
 {
     using S = typename RT<DT>::S;
     using C = typename RT<DT>::C;
-    constexpr int RPB = 4 / WPR;
+    constexpr int RPB = RowShape<WPR>::RPB, BW = RowShape<WPR>::BW;
+    // chunks in flight per lane: 4, or fewer when the row's block is wider
+    constexpr int U = WPR >= 8 ? 2 : 4;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wr = wave % WPR;                        // wave within its row
@@ -324,13 +377,13 @@ __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin
     constexpr int STEP = 64 * VEC;                    // one wave-wide chunk
     constexpr int RSTEP = WPR * STEP;                 // one row-wide chunk
     int i = wr * STEP + lane * VEC;
-    // main loop: 4 chunks in flight per lane
-    for (; i + 3 * RSTEP + VEC <= n; i += 4 * RSTEP) {
-        C v[4][VEC];
+    // main loop: U chunks in flight per lane
+    for (; i + (U - 1) * RSTEP + VEC <= n; i += U * RSTEP) {
+        C v[U][VEC];
 #pragma unroll
-        for (int u = 0; u < 4; u++) load_chunk<DT, VEC>(x + i + u * RSTEP, v[u]);
+        for (int u = 0; u < U; u++) load_chunk<DT, VEC>(x + i + u * RSTEP, v[u]);
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             if constexpr (OP == R_VAR) {
                 var_add_chunk<C, VEC>(acc, v[u], VEC);
             } else {
@@ -358,7 +411,7 @@ __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin
 #pragma unroll
         for (int s = 32; s >= 1; s >>= 1) m = mom_combine(m, mom_shfl(m, s));
         if constexpr (WPR > 1) {
-            __shared__ LdsSlot<Mom> part[4];
+            __shared__ LdsSlot<Mom> part[BW];
             if (lane == 0) *reinterpret_cast<Mom *>(part[wave].raw) = m;
             __syncthreads();
             if (wr != 0) return;
@@ -371,7 +424,7 @@ __global__ __launch_bounds__(256) void k_row_reduce(const void *__restrict__ xin
     } else {
         wave_merge(acc);
         if constexpr (WPR > 1) {
-            __shared__ LdsSlot<Acc<C, OP>> part[4];
+            __shared__ LdsSlot<Acc<C, OP>> part[BW];
             if (lane == 0) memcpy(part[wave].raw, &acc, sizeof(acc));
             __syncthreads();
             if (wr != 0) return;
@@ -471,20 +524,103 @@ __device__ __forceinline__ void store_row(OS *y, int n, int wr, int lane, bool f
 // result definition as the Welford kernels (M2 / (n - correction), sqrt for
 // std), one HBM pass.
 template <int DT, int VEC, int NCH, int WPR>
-__global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xin, size_t rows, int n,
-                                                     size_t ld, void *__restrict__ out, int out_dt,
-                                                     int correction, int take_sqrt)
+__global__ __launch_bounds__(64 * RowShape<WPR>::BW) void k_row_moments(const void *__restrict__ xin, size_t rows,
+                                                                         int n, size_t ld, void *__restrict__ out,
+                                                                         int out_dt, int correction, int take_sqrt)
 {
     using S = typename RT<DT>::S;
     using C = typename RT<DT>::C;
-    __shared__ C lds[4];
+    __shared__ C lds[RowShape<WPR>::BW];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6, wr = wave % WPR;
-    const size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    const size_t row = (size_t)blockIdx.x * RowShape<WPR>::RPB + wave / WPR;
     if (row >= rows) return;  // WPR > 1: one row per block, never taken
     const S *x = (const S *)xin + row * ld;
     C v[NCH][VEC];
     const bool full = load_row<DT, VEC, NCH, WPR, true>(x, n, wr, lane, (C)0, v);
+    if (n == NCH * VEC * 64 * WPR) {
+        // Every lane holds NCH * VEC elements: exact two-pass over the
+        // lane's own values, then Chan's pairwise combination of
+        // (mean, M2) states of equal counts over the lanes (butterfly: both
+        // partners compute the same sums, so every lane ends with the wave's
+        // state) and over the waves, in double, by one lane: one exchange
+        // through LDS instead of a row mean followed by a row sum.
+        constexpr int NL = NCH * VEC;
+        C ls = 0;
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int k = 0; k < VEC; k++) ls = ls + v[c][k];
+        C mean = ls / (C)NL, q = 0;
+#pragma unroll
+        for (int c = 0; c < NCH; c++)
+#pragma unroll
+            for (int k = 0; k < VEC; k++) {
+                const C d = v[c][k] - mean;
+                q = q + d * d;
+            }
+        C cnt = (C)NL;
+        // equal-count combination of the partner's state (om, oq)
+        auto chan = [&](C om, C oq) {
+            const C d = om - mean;
+            q = (q + oq) + d * d * (cnt * (C)0.5);
+            mean = (mean + om) * (C)0.5;
+            cnt = cnt * 2;
+        };
+        if constexpr (sizeof(C) == 4) {
+            // lanes ^ 1, ^ 2 (DPP quad permutes), then the half-row and row
+            // mirrors (as in wave_all), then the four row states in order
+            auto dpp = [](C x, auto CTRL) {
+                return __builtin_bit_cast(C, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                          decltype(CTRL)::value, 0xF, 0xF, false));
+            };
+            chan(dpp(mean, std::integral_constant<int, 0xB1>{}), dpp(q, std::integral_constant<int, 0xB1>{}));
+            chan(dpp(mean, std::integral_constant<int, 0x4E>{}), dpp(q, std::integral_constant<int, 0x4E>{}));
+            chan(dpp(mean, std::integral_constant<int, 0x141>{}), dpp(q, std::integral_constant<int, 0x141>{}));
+            chan(dpp(mean, std::integral_constant<int, 0x140>{}), dpp(q, std::integral_constant<int, 0x140>{}));
+            auto rl = [](C x, int l) {
+                return __builtin_bit_cast(C, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+            };
+            const C m16 = rl(mean, 16), q16 = rl(q, 16), m32 = rl(mean, 32), q32 = rl(q, 32);
+            const C m48 = rl(mean, 48), q48 = rl(q, 48);
+            mean = rl(mean, 0);
+            q = rl(q, 0);
+            const C c16 = cnt;
+            chan(m16, q16);  // rows 0 + 1
+            const C ma = mean, qa = q;
+            mean = m32;
+            q = q32;
+            cnt = c16;
+            chan(m48, q48);  // rows 2 + 3
+            chan(ma, qa);    // (rows 2 + 3) + (rows 0 + 1): equal counts, symmetric
+        } else {
+#pragma unroll
+            for (int sh = 32; sh >= 1; sh >>= 1) chan(__shfl_xor(mean, sh, PT_WAVE), __shfl_xor(q, sh, PT_WAVE));
+        }
+        if constexpr (WPR > 1) {
+            __shared__ C part_m[RowShape<WPR>::BW], part_q[RowShape<WPR>::BW];
+            if (lane == 0) {
+                part_m[wave] = mean;
+                part_q[wave] = q;
+            }
+            __syncthreads();
+            if (wr != 0 || lane != 0) return;
+            double dm = (double)mean, dq = (double)q, dn = (double)cnt;
+            for (int w = 1; w < WPR; w++) {
+                const double om = (double)part_m[wave + w], oq = (double)part_q[wave + w], on = (double)cnt;
+                const double nn = dn + on, d = om - dm;
+                dm = dm + d * (on / nn);
+                dq = dq + oq + d * d * (dn * on / nn);
+                dn = nn;
+            }
+            const double var = dq / (double)(n - correction);
+            store_out(out, out_dt, row, take_sqrt ? sqrt(var) : var);
+        } else if (lane == 0) {
+            const double var = (double)q / (double)(n - correction);
+            store_out(out, out_dt, row, take_sqrt ? sqrt(var) : var);
+        }
+        return;
+    }
     C s = 0;
 #pragma unroll
     for (int c = 0; c < NCH; c++)
@@ -527,16 +663,17 @@ __global__ __launch_bounds__(256) void k_row_moments(const void *__restrict__ xi
 // (rows blockIdx.x, + gridDim.x, ...) and issues the next row's loads before
 // the current row's reductions, so HBM stays busy across its two passes.
 template <int DT, int VEC, int NCH, int WPR, typename OS, bool LNT = false, bool SNT = false, bool RW = false>
-__global__ __launch_bounds__(256) void k_row_softmax(const void *__restrict__ xin, size_t rows,
-                                                     int n, size_t ld, OS *__restrict__ out)
+__global__ __launch_bounds__(64 * RowShape<WPR>::BW) void k_row_softmax(const void *__restrict__ xin, size_t rows,
+                                                                         int n, size_t ld, OS *__restrict__ out)
 {
     using S = typename RT<DT>::S;
     using C = typename RT<DT>::C;
-    __shared__ C lds[4];
+    constexpr int RPB = RowShape<WPR>::RPB;
+    __shared__ C lds[RowShape<WPR>::BW];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6, wr = wave % WPR;
-    size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
-    const size_t row_step = RW ? (size_t)gridDim.x * (4 / WPR) : rows;
+    size_t row = (size_t)blockIdx.x * RPB + wave / WPR;
+    const size_t row_step = RW ? (size_t)gridDim.x * RPB : rows;
     if (row >= rows) return;  // WPR > 1: uniform per block
     const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, 63) + VEC <= n;  // wave-uniform
     C nx[NCH][VEC];
@@ -627,16 +764,17 @@ __device__ __forceinline__ void load_vec16(const T *p, T (&v)[VEC])
 // chunks in registers across them, so they are read once per block instead
 // of once per row.
 template <int DT, int VEC, int NCH, int WPR, typename CT, bool LNT = false, bool SNT = false>
-__global__ __launch_bounds__(256) void k_row_layernorm(const void *__restrict__ xin, size_t rows,
-                                                       int n, CT eps, const CT *__restrict__ gamma,
-                                                       const CT *__restrict__ beta,
-                                                       CT *__restrict__ out)
+__global__ __launch_bounds__(64 * RowShape<WPR>::BW) void k_row_layernorm(const void *__restrict__ xin, size_t rows,
+                                                                           int n, CT eps,
+                                                                           const CT *__restrict__ gamma,
+                                                                           const CT *__restrict__ beta,
+                                                                           CT *__restrict__ out)
 {
     using S = typename RT<DT>::S;
-    __shared__ CT lds[4];
+    __shared__ CT lds[RowShape<WPR>::BW];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6, wr = wave % WPR;
-    size_t row = (size_t)blockIdx.x * (4 / WPR) + wave / WPR;
+    size_t row = (size_t)blockIdx.x * RowShape<WPR>::RPB + wave / WPR;
     const size_t row_step = WPR > 1 ? (size_t)gridDim.x : rows;
     if (row >= rows) return;  // WPR > 1: uniform per block
     const bool full = chunk_start<VEC, WPR>(NCH - 1, wr, 63) + VEC <= n;  // wave-uniform
@@ -1398,12 +1536,44 @@ static bool as_rows(const int *shape, const size_t *strides, int ndims, int axis
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Waves per row of the block-per-row kernels on fp32 rows of 5 to 16
+// chunks of 16 bytes per wave-row step (up to 4096 floats): 8 for sum /
+// mean / max / min / prod, variance, softmax and layerNorm, 4 for argmax /
+// argmin.  On config 2 (X[8192, 4096]) against 4 waves: sum 20.5 against
+// 20.8 us, softmax 41.6 against 42.9 us, layerNorm 43.4 against 43.9 us,
+// variance (single-exchange Chan merge) 20.9-21.0 against 21.1; argmax took
+// 22.8 against 21.3 us.  16 waves (1024-thread blocks) ran 30-60 % slower for every op,
+// and nontemporal row loads or stores slowed softmax and layerNorm at every
+// width.  PT_ROW_WAVES (4 or 8) overrides the choice, a tuning knob read
+// once from the environment.
+static int row_waves(bool arg)
+{
+    static const int w = [] {
+        const char *e = getenv("PT_ROW_WAVES");
+        const int v = e && *e ? atoi(e) : 0;
+        return (v == 4 || v == 8) ? v : 0;
+    }();
+    return w ? w : arg ? 4 : 8;
+}
+
 template <int DT, int OP>
 static void launch_rows_t(const void *x, size_t rows, int n, size_t ld, void *out, int out_dt,
                           int correction, int take_sqrt, hipStream_t s)
 {
     constexpr int V = RT<DT>::V;
     dim3 block(256);
+    if constexpr (DT == PT_FLOAT32) {
+        const int chunks = (n + 64 * V - 1) / (64 * V);
+        if (row_waves(OP == R_ARGMAX || OP == R_ARGMIN) == 8 && n % V == 0 && ld % V == 0 && aligned16(x) &&
+            chunks > 4 && chunks <= 16) {
+            dim3 grid1((unsigned)rows), block8(512);
+            if constexpr (OP == R_VAR)
+                k_row_moments<DT, V, 2, 8><<<grid1, block8, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+            else
+                k_row_reduce<DT, OP, V, 8><<<grid1, block8, 0, s>>>(x, rows, n, ld, out, out_dt, 0, 0);
+            return;
+        }
+    }
     if constexpr (OP == R_VAR) {
         // rows that fit in registers: two-pass moments, one block per row
         int chunks = (n + 64 * V - 1) / (64 * V);
@@ -1688,6 +1858,12 @@ static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS
     dim3 block(256), grid4((unsigned)((rows + 3) / 4)), grid1((unsigned)rows);
     bool vec = n % V == 0 && ld % V == 0 && aligned16(x) && aligned16(y);
     int chunks = (n + 64 * V - 1) / (64 * V);
+    if constexpr (DT == PT_FLOAT32) {
+        if (vec && chunks > 4 && chunks <= 16 && row_waves(false) == 8) {
+            k_row_softmax<DT, V, 2, 8, OS><<<grid1, dim3(512), 0, s>>>(x, rows, n, ld, y);
+            return;
+        }
+    }
     if (vec) {
         switch (chunks) {
         case 1: k_row_softmax<DT, V, 1, 1, OS><<<grid4, block, 0, s>>>(x, rows, n, ld, y); return;
@@ -1712,7 +1888,7 @@ static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS
 // 44.3-44.4 us with 2048 blocks (768 resident) and 43.3-43.4 us with 768,
 // 1536 or 3072.  The count is taken once per kernel, on the first device
 // that launches it (every device of a host is the same model here).
-template <auto K>
+template <auto K, int THREADS = 256>
 static unsigned walk_grid(size_t rows)
 {
     static const unsigned resident = [] {
@@ -1720,7 +1896,7 @@ static unsigned walk_grid(size_t rows)
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, K, 256, 0) != hipSuccess || per_cu < 1)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, K, THREADS, 0) != hipSuccess || per_cu < 1)
             per_cu = 1;
         (void)hipGetLastError();  // a failed query is not the launch's error
         return (unsigned)(per_cu * cus);
@@ -1738,6 +1914,13 @@ static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, con
     bool vec = n % V == 0 && aligned16(x) && aligned16(y) && (!g || aligned16(g)) &&
                (!b || aligned16(b));
     int chunks = (n + 64 * V - 1) / (64 * V);
+    if constexpr (DT == PT_FLOAT32 && sizeof(CT) == 4) {
+        if (vec && chunks > 4 && chunks <= 16 && row_waves(false) == 8) {
+            constexpr auto k = k_row_layernorm<DT, V, 2, 8, CT>;
+            k<<<walk_grid<k, 512>(rows), dim3(512), 0, s>>>(x, rows, n, eps, g, b, y);
+            return;
+        }
+    }
     if (vec) {
         switch (chunks) {
         case 1: k_row_layernorm<DT, V, 1, 1, CT><<<grid4, block, 0, s>>>(x, rows, n, eps, g, b, y); return;
