@@ -33,8 +33,10 @@ def cross_entropy(scores, labels):
     return float((logz - target).sum())
 
 
-def loss_and_grads(x, labels, params, scale):
-    """Loss and d(loss * scale)/d(params) (backward seeded with `scale`)."""
+def loss_and_grads(x, labels, params, scale, intermediates=None):
+    """Loss and d(loss * scale)/d(params) (backward seeded with `scale`).
+    A dict passed as `intermediates` receives the forward and backward
+    values (z1, h1, z2, h2, scores, d_scores, dh2, dz2, dh1, dz1)."""
     w1, b1, w2, b2, w3, b3 = params
     scores, (z1, h1, z2, h2) = predict(x, params)
     loss = cross_entropy(scores, labels)
@@ -57,6 +59,9 @@ def loss_and_grads(x, labels, params, scale):
     dz1 = np.where(z1 > 0, dh1, 0.0)
     gw1 = x.T @ dz1
     gb1 = dz1.sum(axis=0, keepdims=True)
+    if intermediates is not None:
+        intermediates.update(z1=z1, h1=h1, z2=z2, h2=h2, scores=scores, d_scores=d_scores, dh2=dh2, dz2=dz2,
+                             dh1=dh1, dz1=dz1)
     return loss, [gw1, gb1, gw2, gb2, gw3, gb3]
 
 
