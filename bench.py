@@ -452,7 +452,8 @@ def mlp_family(steps, warmup):
     return {"workload": "config5: MLP 784-1024-1024-10 fp32, batch 4096, softmax-CE, backward, clip 5, AdamW 1e-3",
             "ms_per_step": ms, "TFLOP/s": tf, "frac": tf / PEAK_TFLOPS["fp32"], "flop_per_step": flops,
             "eager_ms_per_step": eager_ms, "plan_steps": len(kinds), "plan_native_steps": kinds.count("native"),
-            "plan_kernels": kinds.count("fused"), "workspace_bytes": graph.getStats().get("workspaceBytes")}
+            "plan_kernels": kinds.count("fused"), "workspace_bytes": graph.getStats().get("workspaceBytes"),
+            "row_chains": graph.getStats().get("rowChains"), "row_chain_steps": graph.getStats().get("rowChainSteps")}
 
 
 # The step's products with the operand layouts the compiled plan hands to

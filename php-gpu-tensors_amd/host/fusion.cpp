@@ -29,6 +29,7 @@
 #include <functional>
 #include <map>
 #include <mutex>
+#include <set>
 #include <sstream>
 #include <unordered_map>
 
@@ -146,6 +147,20 @@ struct Step {
     int item = -1;
 };
 
+// Row chain: plan steps that each work row by row on values of one row
+// count (fused kernels whose reads of the chain's own values stay in the
+// output's row, and native last-axis reductions of short fp32 rows), run by
+// one generated kernel, one wave per row, at the position of the last
+// member.  The plan's steps and their reported form are unchanged; only the
+// number of launches drops.
+struct RowChain {
+    std::vector<int> members;     // step indices, in plan order
+    long long rows = 0;
+    std::vector<char> vec4;       // per member: a reduction whose rows are read as 4-element chunks
+    std::string name;
+    pt_function_t fn = nullptr;
+};
+
 struct Plan {
     std::vector<Item> items;
     std::vector<Kernel> kernels;
@@ -184,6 +199,13 @@ struct Plan {
     // capture into a graph nor run asynchronously
     bool indexed = false;
     std::shared_ptr<Storage> index_record;
+    // row chains (their kernels live in a module of their own, so that the
+    // plan's generated source is what the steps alone produce)
+    std::vector<RowChain> chains;
+    std::vector<int> step_chain;     // per step: chain index, or -1
+    std::string chain_source;
+    pt_module_t chain_module = nullptr;
+    size_t chain_fallbacks = 0;
 };
 
 static bool is_elementwise(const FusionNode &n)
@@ -560,8 +582,10 @@ static void emit_prelude(std::ostringstream &os)
 }
 
 // General path: one device function per node, evaluated at the node's own
-// linear index (as the reference codegen does), scalar accesses.
-static void emit_general(Plan &p, Kernel &k, std::ostringstream &os)
+// linear index (as the reference codegen does), scalar accesses.  The node
+// functions of kernel `k` are named <k.name>_n<item> and take the kernel's
+// leaf pointers p0.. in leaf order, then the index.
+static void emit_node_functions(Plan &p, Kernel &k, std::ostringstream &os)
 {
     std::vector<char> emitted(p.items.size(), 0);
     std::string params;
@@ -634,6 +658,15 @@ static void emit_general(Plan &p, Kernel &k, std::ostringstream &os)
         os << "return " << node_expr(p, id, ops) << ";}\n";
     };
     for (int r : k.roots) emit(r);
+}
+
+static void emit_general(Plan &p, Kernel &k, std::ostringstream &os)
+{
+    emit_node_functions(p, k, os);
+    std::string params;
+    for (size_t l = 0; l < k.leaves.size(); l++) params += "const void* __restrict__ p" + std::to_string(l) + ",";
+    std::string args;
+    for (size_t l = 0; l < k.leaves.size(); l++) args += "p" + std::to_string(l) + ",";
     os << "extern \"C\" __global__ void " << k.name << "_s(" << params;
     for (size_t r = 0; r < k.roots.size(); r++) os << (r ? "," : "") << "void* __restrict__ out" << r;
     os << "){for(unsigned long long i=(unsigned long long)blockIdx.x*blockDim.x+threadIdx.x;i<" << k.total
@@ -980,6 +1013,271 @@ static void output_regions(Plan &p)
 }
 
 // ------------------------------------------------------------ plan build
+// ------------------------------------------------------------ row chains
+// Short rows make short kernels: a step over [4096, 10] values moves 160 KiB
+// and its time is the launch and the first loads of what the step before it
+// has just written.  A run of such steps (a softmax cross-entropy and its
+// backward: row max, shift, exp, row sums, log, the max's gradient shared
+// among ties) is executed by one kernel that gives each row a wave and runs
+// the steps one after the other inside it, each step's stores visible to
+// the next after a workgroup barrier.  Each fused step evaluates the same
+// node functions as its own kernel; each reduction adds in the order of the
+// native row kernel for that row length (k_row_reduce with one wave per
+// row: each lane folds its elements in index order, four-element chunks
+// when the row length is a multiple of 4, then the wave's DPP tree), so the
+// chain's values are bit-identical to the steps run one by one.
+
+// Longest row (elements) a chain takes: at most four values per lane, and
+// the native reduction of such a row runs one wave per row.
+static constexpr long long kChainRowMax = 256;
+
+static bool row_chains_enabled()
+{
+    // PT_FUSION_ROW_CHAINS=0 runs every step by itself (a tuning and test
+    // knob, read once from the environment)
+    static const bool on = [] {
+        const char *e = getenv("PT_FUSION_ROW_CHAINS");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// How kernel `k` reads its leaves relative to its output rows.  A leaf
+// reached only through index maps that send output row r into row r of the
+// leaf (equal shapes, broadcasts that keep the leading row dimension,
+// reshapes that keep the row-major order) gets RL_ROW; any other path adds
+// RL_OTHER.
+enum { RL_ROW = 1, RL_OTHER = 2 };
+
+static void row_reads(const Plan &p, const Kernel &k, int id, int state, long long rows, std::map<int, int> &leaf,
+                      std::set<std::pair<int, int>> &seen)
+{
+    if (!seen.insert({id, state}).second) return;
+    if (is_leaf(p, k, id)) {
+        leaf[id] |= state;
+        return;
+    }
+    const Item &it = p.items[id];
+    const Tensor &t = *it.t;
+    const FusionNode &n = *t.node;
+    for (int a : it.args) {
+        const Tensor &c = *p.items[a].t;
+        int cs = RL_OTHER;
+        if (state == RL_ROW) {
+            if (n.kind == N_VIEW) {
+                // source index = offset + sum coord_d * view_stride_d.  It
+                // stays in the row when the view's leading dimension is the
+                // rows, one view row steps one source row, and the other
+                // dimensions reach less than a source row (reshapes to
+                // [rows, 1], broadcasts of [rows, 1] to [rows, n]); or when
+                // the view keeps the row-major order (offset 0, the view
+                // shape's contiguous strides).
+                const size_t total = c.numel();
+                bool row = t.ndims >= 1 && t.shape[0] == rows && total % (size_t)rows == 0 &&
+                           n.view_offset == 0 && n.view_strides[0] == total / (size_t)rows;
+                size_t reach = 0;
+                for (int d = 1; d < t.ndims && row; d++) {
+                    if (t.shape[d] <= 1) continue;
+                    if (n.view_strides[d] >= total) row = false;
+                    else reach += (size_t)(t.shape[d] - 1) * n.view_strides[d];
+                }
+                row = row && reach < total / (size_t)rows;
+                size_t cst[kMaxDims];
+                contiguous_strides(t.shape, t.ndims, cst);
+                bool same = n.view_offset == 0 && total == t.numel();
+                for (int d = 0; d < t.ndims && same; d++)
+                    if (t.shape[d] > 1 && n.view_strides[d] != cst[d]) same = false;
+                if (row || same) cs = RL_ROW;
+            } else {
+                const bool eq = c.ndims == t.ndims && std::equal(c.shape, c.shape + c.ndims, t.shape);
+                const bool lead = c.ndims == t.ndims && t.shape[0] == rows && c.shape[0] == rows;
+                if (eq || lead) cs = RL_ROW;
+            }
+        }
+        row_reads(p, k, a, cs, rows, leaf, seen);
+    }
+}
+
+// Rows of a fused step that may join a chain (0: it may not).
+static long long kernel_rows(const Kernel &k)
+{
+    if (k.ndims < 1 || k.total == 0) return 0;
+    const long long rows = k.shape[0];
+    if (rows < 2 || rows > 0x7fffffffLL || (long long)k.total / rows > kChainRowMax) return 0;
+    return rows;
+}
+
+// A native step that may join a chain: a float32 sum / mean / max / min /
+// product over the last axis of a materialized [rows, n] float32 value.
+static bool chain_reduction(const Plan &p, const Step &st, long long &rows, long long &n)
+{
+    const Item &it = p.items[st.item];
+    const NativeSpec &ns = it.t->node->native;
+    if (ns.kind != NAT_REDUCE || it.args.size() != 1 || it.t->dtype != PT_FLOAT32) return false;
+    if (ns.op != PT_OP_REDUCE_SUM && ns.op != PT_OP_REDUCE_MEAN && ns.op != PT_OP_REDUCE_MAX &&
+        ns.op != PT_OP_REDUCE_MIN && ns.op != PT_OP_REDUCE_PROD)
+        return false;
+    const Item &a = p.items[it.args[0]];
+    if (!(a.kind == IT_NATIVE || (a.kind == IT_ELEM && a.cut))) return false;
+    const Tensor &x = *a.t;
+    if (x.dtype != PT_FLOAT32 || x.ndims != 2 || ns.axis != 1) return false;
+    rows = x.shape[0];
+    n = x.shape[1];
+    return rows >= 2 && rows <= 0x7fffffffLL && n >= 1 && n <= kChainRowMax;
+}
+
+static void emit_row_chain(Plan &p, const RowChain &ch, std::ostringstream &os)
+{
+    for (int m : ch.members)
+        if (!p.steps[m].native) emit_node_functions(p, p.kernels[p.steps[m].kernel], os);
+    // no __restrict__: a member reads what an earlier member wrote, through
+    // another parameter
+    std::string params;
+    auto param = [&](const std::string &decl) { params += (params.empty() ? "" : ",") + decl; };
+    for (size_t j = 0; j < ch.members.size(); j++) {
+        const Step &st = p.steps[ch.members[j]];
+        const std::string m = "m" + std::to_string(j);
+        if (st.native) {
+            param("const void* " + m + "_x");
+            param("void* " + m + "_o0");
+        } else {
+            const Kernel &k = p.kernels[st.kernel];
+            for (size_t l = 0; l < k.leaves.size(); l++) param("const void* " + m + "_p" + std::to_string(l));
+            for (size_t r = 0; r < k.roots.size(); r++) param("void* " + m + "_o" + std::to_string(r));
+        }
+    }
+    os << "extern \"C\" __global__ __launch_bounds__(64) void " << ch.name << "(" << params << "){\n"
+       << "const unsigned lane=threadIdx.x;\nconst unsigned long long row=blockIdx.x;\n";
+    for (size_t j = 0; j < ch.members.size(); j++) {
+        const Step &st = p.steps[ch.members[j]];
+        const std::string m = "m" + std::to_string(j);
+        if (st.native) {
+            long long rows = 0, n = 0;
+            chain_reduction(p, st, rows, n);
+            const int op = p.items[st.item].t->node->native.op;
+            const char *f = op == PT_OP_REDUCE_MAX ? "pt_rc_max" : op == PT_OP_REDUCE_MIN ? "pt_rc_min"
+                          : op == PT_OP_REDUCE_PROD ? "pt_rc_mul" : "pt_rc_add";
+            const char *ident = op == PT_OP_REDUCE_MAX ? "-__builtin_inff()" : op == PT_OP_REDUCE_MIN ? "__builtin_inff()"
+                              : op == PT_OP_REDUCE_PROD ? "1.0f" : "0.0f";
+            os << "{const float* x=static_cast<const float*>(" << m << "_x)+row*" << n << "ULL;\nfloat a=" << ident
+               << ";\n";
+            if (ch.vec4[j])
+                os << "for(unsigned e=4u*lane;e<" << n << "u;e+=256u){a=" << f << "(a,x[e]);a=" << f << "(a,x[e+1]);a="
+                   << f << "(a,x[e+2]);a=" << f << "(a,x[e+3]);}\n";
+            else
+                os << "for(unsigned e=lane;e<" << n << "u;e+=64u)a=" << f << "(a,x[e]);\n";
+            os << "a=pt_rc_wave(a," << f << ");\n";
+            if (op == PT_OP_REDUCE_MEAN) os << "a=a/(float)" << n << ";\n";
+            os << "if(lane==0)static_cast<float*>(" << m << "_o0)[row]=a;}\n";
+        } else {
+            const Kernel &k = p.kernels[st.kernel];
+            const long long n = (long long)k.total / ch.rows;
+            std::string args;
+            for (size_t l = 0; l < k.leaves.size(); l++) args += m + "_p" + std::to_string(l) + ",";
+            os << "for(unsigned long long e=lane;e<" << n << "ULL;e+=64ULL){\nconst unsigned long long i=row*" << n
+               << "ULL+e;\n";
+            for (size_t r = 0; r < k.roots.size(); r++) {
+                const Tensor &t = *p.items[k.roots[r]].t;
+                os << "static_cast<" << storage_type(t.dtype) << "*>(" << m << "_o" << r << ")[i]="
+                   << store_conv(t.dtype, k.name + "_n" + std::to_string(k.roots[r]) + "(" + args + "i)") << ";\n";
+            }
+            os << "}\n";
+        }
+        if (j + 1 < ch.members.size()) os << "__syncthreads();\n";
+    }
+    os << "}\n";
+}
+
+static void find_row_chains(Plan &p)
+{
+    const int ns = (int)p.steps.size();
+    p.step_chain.assign(ns, -1);
+    if (!row_chains_enabled() || ns < 2) return;
+    const int nitems = (int)p.items.size();
+    std::vector<int> producer(nitems, -1);
+    for (int i = 0; i < ns; i++) {
+        const Step &st = p.steps[i];
+        if (st.native) producer[st.item] = i;
+        else
+            for (int r : p.kernels[st.kernel].roots) producer[r] = i;
+    }
+    // rows of step i as a member of a chain whose steps are marked in
+    // `in_chain` (0: it cannot join); a fused step must read every value
+    // the chain produces within the row
+    auto member_rows = [&](int i, const std::vector<char> &in_chain, char &vec4) -> long long {
+        const Step &st = p.steps[i];
+        vec4 = 0;
+        if (st.native) {
+            long long rows = 0, n = 0;
+            if (!chain_reduction(p, st, rows, n)) return 0;
+            // the native row kernel reads 16-byte chunks of such rows
+            vec4 = n % 4 == 0;
+            return rows;
+        }
+        const Kernel &k = p.kernels[st.kernel];
+        const long long rows = kernel_rows(k);
+        if (!rows) return 0;
+        std::map<int, int> leaf;
+        std::set<std::pair<int, int>> seen;
+        for (int r : k.roots) row_reads(p, k, r, RL_ROW, rows, leaf, seen);
+        for (const auto &e : leaf) {
+            const int pr = producer[e.first];
+            if (pr >= 0 && in_chain[pr] && e.second != RL_ROW) return 0;
+        }
+        return rows;
+    };
+    // A chain is a run of consecutive steps: the plan's order, and the
+    // branch each step runs on, stay as they are, with the run collapsed
+    // into one launch at its last step.
+    int next_free = 0;
+    for (int s0 = 0; s0 < ns; s0++) {
+        if (s0 < next_free) continue;
+        std::vector<char> in_chain(ns, 0);
+        char v4 = 0;
+        const long long rows = member_rows(s0, in_chain, v4);
+        if (!rows) continue;
+        RowChain ch;
+        ch.rows = rows;
+        ch.members = {s0};
+        ch.vec4 = {v4};
+        in_chain[s0] = 1;
+        for (int j = s0 + 1; j < ns && member_rows(j, in_chain, v4) == rows; j++) {
+            ch.members.push_back(j);
+            ch.vec4.push_back(v4);
+            in_chain[j] = 1;
+        }
+        if (ch.members.size() < 2) continue;
+        const int c = (int)p.chains.size();
+        ch.name = "rc" + std::to_string(c);
+        for (int m : ch.members) p.step_chain[m] = c;
+        next_free = ch.members.back() + 1;
+        p.chains.push_back(ch);
+    }
+    if (p.chains.empty()) return;
+    std::ostringstream os;
+    emit_prelude(os);
+    // the native row kernel's wave reduction (wave_all in pt_common.h): DPP
+    // quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror,
+    // then lanes 0 + 16 and 32 + 48
+    os << "__device__ __forceinline__ float pt_rc_add(float a,float b){return a+b;}\n"
+          "__device__ __forceinline__ float pt_rc_mul(float a,float b){return a*b;}\n"
+          "__device__ __forceinline__ float pt_rc_max(float a,float b){return fmaxf(a,b);}\n"
+          "__device__ __forceinline__ float pt_rc_min(float a,float b){return fminf(a,b);}\n"
+          "template<typename F>__device__ __forceinline__ float pt_rc_wave(float v,F f){\n"
+          "v=f(v,__uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0,(int)__float_as_uint(v),0xB1,0xF,0xF,false)));\n"
+          "v=f(v,__uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0,(int)__float_as_uint(v),0x4E,0xF,0xF,false)));\n"
+          "v=f(v,__uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0,(int)__float_as_uint(v),0x141,0xF,0xF,false)));\n"
+          "v=f(v,__uint_as_float((unsigned)__builtin_amdgcn_update_dpp(0,(int)__float_as_uint(v),0x140,0xF,0xF,false)));\n"
+          "const int iv=(int)__float_as_uint(v);\n"
+          "const float a=__uint_as_float((unsigned)__builtin_amdgcn_readlane(iv,0));\n"
+          "const float b=__uint_as_float((unsigned)__builtin_amdgcn_readlane(iv,16));\n"
+          "const float c=__uint_as_float((unsigned)__builtin_amdgcn_readlane(iv,32));\n"
+          "const float d=__uint_as_float((unsigned)__builtin_amdgcn_readlane(iv,48));\n"
+          "return f(f(a,b),f(c,d));}\n";
+    for (const RowChain &ch : p.chains) emit_row_chain(p, ch, os);
+    p.chain_source = os.str();
+}
+
 static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<TensorP> &inputs)
 {
     auto *p = new Plan();
@@ -1292,6 +1590,7 @@ static Plan *build_plan(const std::vector<TensorP> &roots, const std::vector<Ten
         p->graph_compatible = false;
         p->incompatibility = "indexed-operation";
     }
+    find_row_chains(*p);
     return p;
 }
 
@@ -1376,25 +1675,80 @@ static TensorP native_arg(const Plan &p, std::vector<TensorP> &vals, int id)
     return v;
 }
 
+// One step on the current stream.
+static bool run_step(Plan &p, const Step &st, std::vector<TensorP> &vals)
+{
+    if (!st.native) return launch_kernel(p, p.kernels[st.kernel], vals);
+    Item &it = p.items[st.item];
+    std::vector<TensorP> ins;
+    for (int a : it.args) {
+        TensorP v = native_arg(p, vals, a);
+        if (!v) return false;
+        ins.push_back(v);
+    }
+    preset_output(vals[st.item]);
+    TensorP out = native_execute(it.t->node->native, ins);
+    preset_output(nullptr);
+    if (!out) return false;
+    vals[st.item] = out;
+    return true;
+}
+
+// The chain's kernel: one 64-thread workgroup per row.  A reduction whose
+// chunked order was assumed needs its rows 16-byte aligned, as the native
+// kernel does to read them in chunks; otherwise `launched` stays false.
+static bool launch_chain(Plan &p, RowChain &ch, std::vector<TensorP> &vals, bool &launched)
+{
+    launched = false;
+    std::vector<void *> ptrs;
+    for (size_t j = 0; j < ch.members.size(); j++) {
+        const Step &st = p.steps[ch.members[j]];
+        if (st.native) {
+            TensorP x = native_arg(p, vals, p.items[st.item].args[0]);
+            if (!x) return false;
+            const void *xp = x->data();
+            if (ch.vec4[j] && ((uintptr_t)xp & 15u)) return true;
+            ptrs.push_back(const_cast<void *>(xp));
+            ptrs.push_back(vals[st.item]->data());
+        } else {
+            const Kernel &k = p.kernels[st.kernel];
+            for (int l : k.leaves) ptrs.push_back(const_cast<void *>(leaf_ptr(p, vals, l)));
+            for (int r : k.roots) ptrs.push_back(vals[r]->data());
+        }
+    }
+    std::vector<void *> params;
+    for (void *&q : ptrs) params.push_back(&q);
+    launched = true;
+    return check_status(pt_launch(ch.fn, (unsigned)ch.rows, 64, params.data(), nullptr),
+                        "Fusion row-chain launch failed");
+}
+
+// A chain at the position of its last member: its kernel, or its members
+// one by one (no chain kernel, or rows it cannot take).
+static bool run_chain(Plan &p, int c, std::vector<TensorP> &vals)
+{
+    RowChain &ch = p.chains[c];
+    bool launched = false;
+    if (ch.fn && !launch_chain(p, ch, vals, launched)) return false;
+    if (launched) return true;
+    p.chain_fallbacks++;
+    for (int m : ch.members)
+        if (!run_step(p, p.steps[m], vals)) return false;
+    return true;
+}
+
+// Chain of step i, or -1.
+static int chain_of(const Plan &p, int i) { return p.step_chain.empty() ? -1 : p.step_chain[i]; }
+
 static bool run_steps(Plan &p, std::vector<TensorP> &vals)
 {
-    for (Step &st : p.steps) {
-        if (st.native) {
-            Item &it = p.items[st.item];
-            std::vector<TensorP> ins;
-            for (int a : it.args) {
-                TensorP v = native_arg(p, vals, a);
-                if (!v) return false;
-                ins.push_back(v);
-            }
-            preset_output(vals[st.item]);
-            TensorP out = native_execute(it.t->node->native, ins);
-            preset_output(nullptr);
-            if (!out) return false;
-            vals[st.item] = out;
-        } else {
-            if (!launch_kernel(p, p.kernels[st.kernel], vals)) return false;
+    for (int i = 0; i < (int)p.steps.size(); i++) {
+        const int c = chain_of(p, i);
+        if (c >= 0) {
+            if (i == p.chains[c].members.back() && !run_chain(p, c, vals)) return false;
+            continue;
         }
+        if (!run_step(p, p.steps[i], vals)) return false;
     }
     return true;
 }
@@ -1428,12 +1782,16 @@ static bool branch_streams(std::vector<pt_stream_t> &streams)
 static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<pt_event_t> &events)
 {
     const int ns = (int)p.steps.size();
+    // a chain member's values are produced where the chain runs: at its
+    // last member
     std::vector<int> producer(p.items.size(), -1);
     for (int i = 0; i < ns; i++) {
         const Step &st = p.steps[i];
-        if (st.native) producer[st.item] = i;
+        const int c = chain_of(p, i);
+        const int at = c >= 0 ? p.chains[c].members.back() : i;
+        if (st.native) producer[st.item] = at;
         else
-            for (int r : p.kernels[st.kernel].roots) producer[r] = i;
+            for (int r : p.kernels[st.kernel].roots) producer[r] = at;
     }
     auto source = [&](int id) {
         // an uncut view chain handed to a native reads the item it views
@@ -1457,13 +1815,22 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
     std::vector<pt_event_t> done(ns, nullptr);
     for (int i = 0; i < ns && ok; i++) {
         const Step &st = p.steps[i];
+        const int chain = chain_of(p, i);
+        if (chain >= 0 && i != p.chains[chain].members.back()) continue;
         std::vector<int> deps;
-        if (st.native) {
-            for (int a : p.items[st.item].args) deps.push_back(producer[source(a)]);
-        } else {
-            for (int l : p.kernels[st.kernel].leaves) deps.push_back(producer[l]);
-        }
+        auto step_deps = [&](const Step &s) {
+            if (s.native) {
+                for (int a : p.items[s.item].args) deps.push_back(producer[source(a)]);
+            } else {
+                for (int l : p.kernels[s.kernel].leaves) deps.push_back(producer[l]);
+            }
+        };
+        if (chain >= 0)
+            for (int m : p.chains[chain].members) step_deps(p.steps[m]);
+        else
+            step_deps(st);
         deps.erase(std::remove(deps.begin(), deps.end(), -1), deps.end());
+        deps.erase(std::remove(deps.begin(), deps.end(), i), deps.end());
         int latest = deps.empty() ? -1 : *std::max_element(deps.begin(), deps.end());
         int b = -1;
         if (latest >= 0 && last[branch[latest]] == latest) b = branch[latest];
@@ -1482,27 +1849,7 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
         branch[i] = b;
         last[b] = i;
         pt_stream_set_current(streams[b]);
-        if (st.native) {
-            Item &it = p.items[st.item];
-            std::vector<TensorP> ins;
-            for (int a : it.args) {
-                TensorP v = native_arg(p, vals, a);
-                if (!v) {
-                    ok = false;
-                    break;
-                }
-                ins.push_back(v);
-            }
-            if (ok) {
-                preset_output(vals[st.item]);
-                TensorP out = native_execute(it.t->node->native, ins);
-                preset_output(nullptr);
-                if (!out) ok = false;
-                else vals[st.item] = out;
-            }
-        } else {
-            ok = launch_kernel(p, p.kernels[st.kernel], vals);
-        }
+        ok = chain >= 0 ? run_chain(p, chain, vals) : run_step(p, st, vals);
         pt_stream_set_current(nullptr);
         if (ok) ok = new_event(done[i]) && check_status(pt_event_record(done[i], streams[b]), "Fusion branch event");
     }
@@ -1787,17 +2134,48 @@ static bool collect_outputs(Plan &p, std::vector<TensorP> &vals, std::vector<Ten
     return true;
 }
 
+// Row-chain modules, by source.  Kept apart from the Fusion module cache,
+// whose statistics describe the plans' own generated sources; modules stay
+// loaded (plans hold their handles), and past kChainModules sources new
+// chains compile without being kept.
+static std::mutex g_chain_mu;
+static std::unordered_map<std::string, pt_module_t> g_chain_modules;
+static constexpr size_t kChainModules = 64;
+
+static pt_module_t load_chain_module(const std::string &src)
+{
+    std::lock_guard<std::mutex> lock(g_chain_mu);
+    auto it = g_chain_modules.find(src);
+    if (it != g_chain_modules.end()) return it->second;
+    pt_module_t m = nullptr;
+    static char log[8192];
+    if (!check_status(pt_rtc_compile(src.c_str(), "fusion_rows.hip", &m, log, sizeof(log)),
+                      "Fusion row-chain compilation failed"))
+        return nullptr;
+    if (g_chain_modules.size() < kChainModules) g_chain_modules[src] = m;
+    return m;
+}
+
 static bool compile_plan(Plan &p)
 {
-    if (p.kernels.empty()) return true;
-    p.module = load_module(p.source, p.cache_hit);
-    if (!p.module) return false;
-    for (Kernel &k : p.kernels) {
-        if (k.affine &&
-            !check_status(pt_module_function(p.module, (k.name + "_v").c_str(), &k.fn_vec), "Fusion kernel lookup"))
-            return false;
-        if (!check_status(pt_module_function(p.module, (k.name + "_s").c_str(), &k.fn_scalar), "Fusion kernel lookup"))
-            return false;
+    if (!p.kernels.empty()) {
+        p.module = load_module(p.source, p.cache_hit);
+        if (!p.module) return false;
+        for (Kernel &k : p.kernels) {
+            if (k.affine && !check_status(pt_module_function(p.module, (k.name + "_v").c_str(), &k.fn_vec),
+                                          "Fusion kernel lookup"))
+                return false;
+            if (!check_status(pt_module_function(p.module, (k.name + "_s").c_str(), &k.fn_scalar),
+                              "Fusion kernel lookup"))
+                return false;
+        }
+    }
+    if (!p.chains.empty()) {
+        p.chain_module = load_chain_module(p.chain_source);
+        if (!p.chain_module) return false;
+        for (RowChain &ch : p.chains)
+            if (!check_status(pt_module_function(p.chain_module, ch.name.c_str(), &ch.fn), "Fusion row-chain lookup"))
+                return false;
     }
     return true;
 }
@@ -2142,6 +2520,32 @@ const char *phpt_graph_stats(phpt_graph *g)
        << ";workspaceBytes=" << (p.workspace ? p.workspace_bytes : 0) << ";profiling=" << (p.profiling ? 1 : 0)
        << ";profiledExecutions=" << p.profiled << ";bindTimeNs=" << p.bind_ns
        << ";executeTimeNs=" << p.execute_ns << ";collectTimeNs=" << p.collect_ns << ";";
+    // row chains: kernels that each run a run of short-row steps; their
+    // members by getPlan step number ("2.3.5/9.10": two chains)
+    size_t chained = 0;
+    for (const RowChain &ch : p.chains) chained += ch.members.size();
+    std::vector<int> number(p.steps.size(), 0);
+    {
+        int n = 0;
+        std::vector<char> shown(p.items.size(), 0);
+        for (size_t i = 0; i < p.steps.size(); i++) {
+            if (p.steps[i].native)
+                for (int a : p.items[p.steps[i].item].args)
+                    if (p.items[a].alias && !p.items[a].cut && !shown[a]) {
+                        shown[a] = 1;
+                        n++;
+                    }
+            number[i] = n++;
+        }
+    }
+    std::string members;
+    for (const RowChain &ch : p.chains) {
+        if (!members.empty()) members += "/";
+        for (size_t j = 0; j < ch.members.size(); j++)
+            members += (j ? "." : "") + std::to_string(number[ch.members[j]]);
+    }
+    os << "rowChains=" << p.chains.size() << ";rowChainSteps=" << chained << ";rowChainFallbacks=" << p.chain_fallbacks
+       << ";rowChainMembers=" << (members.empty() ? "null" : members) << ";";
     t_text = os.str();
     return t_text.c_str();
 }

@@ -264,6 +264,8 @@ def test_config5_compiled_plan_full_size_vs_oracle():
     p1, s1, loss1 = mlp.unpack_step(graph.run(*inputs))
     stats = graph.getStats()
     assert stats["graphLaunches"] >= 2
+    # the loss chain's [4096, 10] steps run as row chains
+    assert stats["rowChains"] >= 1 and stats["rowChainSteps"] >= 8 and stats["rowChainFallbacks"] == 0
     # the plan's scratch arena holds every native's scratch side by side (a
     # region is not reused within a replay): split-K partials of dW2 (8 x
     # 1024 x 1024 fp32, 33.5 MB), dW1 (9 x 784 x 1024, 28.9 MB) and dW3
