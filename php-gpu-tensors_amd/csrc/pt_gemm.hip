@@ -25,6 +25,7 @@
 // their XCD's L2.
 #include "pt_common.h"
 
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -764,6 +765,18 @@ static const TileInfo kTiles[TILE_COUNT] = {
 
 static int g_tile_override = -1;
 
+// Workgroups a split-K product aims for (512: two per CU).  PT_SPLITK_WORKGROUPS
+// overrides it, a tuning knob read once from the environment.
+static long long splitk_workgroups()
+{
+    static const long long w = [] {
+        const char *e = getenv("PT_SPLITK_WORKGROUPS");
+        const long long v = e && *e ? atoll(e) : 0;
+        return v >= 64 && v <= 8192 ? v : 512;
+    }();
+    return w;
+}
+
 // Tiles chosen by pt_matmul_tune, per (dtype, M, N, K, batch, layout).
 static std::mutex g_tuned_mu;
 static std::map<std::string, int> g_tuned;
@@ -1078,7 +1091,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     g.partial = nullptr;
     if (total_tiles < 256 && g.K >= 8 * BK) {
         // whole rounds: about 2 workgroups per CU, never a partial second round
-        long long want = 512 / total_tiles;
+        long long want = splitk_workgroups() / total_tiles;
         long long max_split = g.K / (4 * BK);
         int ks = (int)(want < max_split ? want : max_split);
         if (ks > 64) ks = 64;

@@ -80,16 +80,24 @@ __device__ __forceinline__ void lds_read_tr16(s16x4_t &dst, uint32_t addr)
 // bf16: v_cvt_pk_bf16_f32 rounds to nearest even and quiets NaN exactly as
 // float_to_bf16 does (checked bit for bit over every exponent / top-mantissa
 // pattern with tie, NaN-payload and subnormal low halves).
+// fp16: v_cvt_pk_f16_f32 gives v_cvt_f16_f32's result for every fp32 bit
+// pattern but NaN (checked over all 2^32); a pair holding a NaN, which only
+// a NaN or infinite operand produces, takes float_to_f16's payload rule
+// off the common path.
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi)
 {
+    const f32x2_t v = {lo, hi};
     if constexpr (DT == PT_BFLOAT16) {
-        const f32x2_t v = {lo, hi};
         return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
     } else {
-        return (uint32_t)float_to_f16(lo) | ((uint32_t)float_to_f16(hi) << 16);
+        uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_t));
+        if (__builtin_expect(__builtin_isnan(lo) || __builtin_isnan(hi), 0))
+            h = (uint32_t)float_to_f16(lo) | ((uint32_t)float_to_f16(hi) << 16);
+        return h;
     }
 }
 

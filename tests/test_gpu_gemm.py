@@ -437,6 +437,41 @@ def test_config4_full_size_every_output(A, dt):
     assert bad == 0, f"{bad} outputs outside tolerance (worst {worst:.3g} of the bound)"
 
 
+@pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
+def test_ring_gemm_nan_and_inf_outputs(A, dt):
+    """The 16-bit ring kernel's epilogue on non-finite sums: a NaN planted in
+    a row of A and a column of B, and infinities of both signs beside them,
+    give NaN exactly where the float64 product of the same operands is NaN,
+    infinities of the same sign where it is infinite, and the fp32 /
+    16-bit bar everywhere else (the packed conversion's NaN pairs take the
+    scalar payload rule; every pair of a NaN row holds one)."""
+    from phptensors import synthetic
+    m = n = 4096
+    k = 64
+    a = O.from_storage(O.to_storage(synthetic.normal((1, m, k), 0.0, 1.0, seed=41), dt), dt).astype(np.float64)
+    b = O.from_storage(O.to_storage(synthetic.normal((1, k, n), 0.0, 1.0, seed=42), dt), dt).astype(np.float64)
+    a[0, 5, 3] = np.nan
+    a[0, 100, 7] = np.inf
+    a[0, 101, 7] = -np.inf
+    b[0, 9, 200] = np.nan
+    b[0, 10, 300] = -np.inf
+    b[0, 11, 301] = np.inf
+    a_s, b_s = O.to_storage(a, dt), O.to_storage(b, dt)
+    got = O.from_storage(run(A, a_s, b_s, dt), dt).astype(np.float64)
+    assert A.backend_info().last_matmul.decode().startswith("mfma-lds")
+    with np.errstate(invalid="ignore"):
+        exact = a @ b
+        scale = np.abs(a) @ np.abs(b)
+    nan = np.isnan(exact)
+    assert nan[0, 5].all() and nan[0, :, 200].all() and not nan.all()
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    inf = np.isinf(exact)
+    assert inf.any()
+    np.testing.assert_array_equal(got[inf], exact[inf])
+    fin = ~(nan | inf)
+    assert np.all(np.abs(got[fin] - exact[fin]) <= 1e-2 * np.maximum(np.abs(exact[fin]), scale[fin] / math.sqrt(k)))
+
+
 def test_config1_on_the_gpu(A):
     """Config 1 (A[256,512] @ B[512,256] fp32 U(-1,1) from seed S1 = 1, the
     HostArray product of contiguous_array_ce.c:1295-1343) through the HIP
