@@ -46,10 +46,10 @@ HBM_PEAK_GBS = 8000.0
 # counter reads for a 128 MiB device copy (fetch x 2.0, write x 1.0).
 # Re-measured when a kernel changes.
 PMC_TRAFFIC_BYTES = {
-    "reduce:sum": 134_516_736, "reduce:mean": 134_517_760, "reduce:max": 134_517_760,
-    "reduce:argmax": 134_521_856, "reduce:var": 134_542_336, "reduce:softmax": 268_545_024,
-    "reduce:layernorm": 269_121_536, "fused:tanh_x_plus_y_z": 1_610_682_496,
-    "gemm:bf16": 1_075_905_024, "gemm:fp16": 1_083_517_888, "gemm:fp32": 2_147_847_040,
+    "reduce:sum": 134_491_134, "reduce:mean": 134_492_158, "reduce:max": 134_492_158,
+    "reduce:argmax": 134_511_610, "reduce:var": 134_526_968, "reduce:softmax": 268_507_123,
+    "reduce:layernorm": 269_116_425, "fused:tanh_x_plus_y_z": 1_610_491_925,
+    "gemm:bf16": 1_076_311_046, "gemm:fp16": 1_086_794_548, "gemm:fp32": 2_147_509_052,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol
