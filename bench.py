@@ -296,18 +296,30 @@ def fused_cpu_baseline(sample_rows=512):
             "sample": f"{sample_rows} of 16384 rows of config 3 on one host core; {dt:.2f} s"}
 
 
-def gemm_cpu_baseline(sample_rows=128):
-    """Oracle matmul (sequential fmaf per output, 1 thread) on a row sample of one batch."""
+def cpu_threads():
+    """Host threads for the CPU baselines: the box's CPU share for one GPU
+    (16), or fewer where the host has fewer."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def gemm_cpu_baseline():
+    """Oracle matmul (the HostArray restatement: one sequential fmaf sum per
+    output, contiguous_array_ce.c:1295-1343) on one whole batch of config 4,
+    its outputs split over the host threads; the 32 batches take 32 times as
+    long (BASELINE.md's CPU plan)."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
-    k = n = 2048
-    a = synthetic.normal((32, 2048, k), 0.0, 0.02, seed=4)[0, :sample_rows]
+    m = k = n = 2048
+    threads = cpu_threads()
+    a = synthetic.normal((32, m, k), 0.0, 0.02, seed=4)[0]
     b = synthetic.normal((32, k, n), 0.0, 0.02, seed=5)[0]
     t0 = time.perf_counter()
-    O.matmul(a, b, O.F32)
+    O.matmul(a, b, O.F32, threads=threads)
     dt = time.perf_counter() - t0
-    return {"value": 2.0 * sample_rows * k * n / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
-            "sample": f"fp32, rows 0..{sample_rows - 1} of batch 0 of config 4 on one host core; {dt:.2f} s"}
+    return {"value": 2.0 * m * k * n / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "config_ms": 32 * dt * 1e3,
+            "sample": f"fp32, batch 0 of 32 of config 4 (2048 x 2048 x 2048) on {threads} host threads; {dt:.2f} s; "
+                      f"the 32 batches extrapolate to {32 * dt:.0f} s"}
 
 
 # ---------------------------------------------------------------- config 4
@@ -574,17 +586,17 @@ def transfer_family(steps, nbytes=256 << 20):
     return out
 
 
-def mlp_cpu_baseline(sample_rows=256):
+def mlp_cpu_baseline(sample_rows=4096):
     """The reference's CPU path for the config-5 step: its eight GEMMs at the
-    config-5 shapes through the oracle's HostArray matmul restatement
-    (sequential fmaf, contiguous_array_ce.c:1295-1343), one core, on a row
-    sample.  Every product of the step is linear in the batch rows (M for
-    the forward and input-gradient products, K for the weight gradients), so
-    the sample's rate is the full step's; the elementwise, loss and AdamW
-    work (under 0.1 % of the step's FLOPs) is left out."""
+    config-5 shapes (the full batch of 4096 rows) through the oracle's
+    HostArray matmul restatement (sequential fmaf, contiguous_array_ce.c:
+    1295-1343), the outputs of each product split over the host threads.
+    The elementwise, loss and AdamW work (under 0.1 % of the step's FLOPs)
+    is left out."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     r = sample_rows
+    threads = cpu_threads()
     # (M, K, N): forward x.W1, h1.W2, h2.W3; backward dZ3.W3^T, dZ2.W2^T,
     # h2^T.dZ3, h1^T.dZ2, x^T.dZ1
     shapes = [(r, 784, 1024), (r, 1024, 1024), (r, 1024, 10), (r, 10, 1024), (r, 1024, 1024),
@@ -595,13 +607,13 @@ def mlp_cpu_baseline(sample_rows=256):
                     synthetic.normal((k, n), 0.0, 0.05, seed=70 + i)))
     t0 = time.perf_counter()
     for a, b in ops:
-        O.matmul(a, b, O.F32)
+        O.matmul(a, b, O.F32, threads=threads)
     dt = time.perf_counter() - t0
     flops = sum(2.0 * m * k * n for m, k, n in shapes)
-    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "step_ms_at_4096_rows": dt * 4096 / r * 1e3,
             "sample": f"the step's 8 GEMMs at {r} of 4096 rows through the oracle's HostArray matmul "
-                      f"restatement (sequential fmaf) on one host core; {dt:.2f} s"}
+                      f"restatement (sequential fmaf) on {threads} host threads; {dt:.2f} s"}
 
 
 def _to_bf16(x):

@@ -9,6 +9,7 @@
 #include "hostarray.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -545,18 +546,15 @@ static size_t batch_offset(const int *shape_in, const size_t *strides_in, int nd
 }
 
 /* HostArray::matmul (contiguous_array_ce.c:1295-1343). */
-int or_matmul(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
-              const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
-              int dtype, void *c, const int *shape_c, int nd_c)
+/* Outputs [begin, end) of the product, each one sum of fmaf in k order
+ * (contiguous_array_ce.c:1295-1343). */
+static void matmul_range(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
+                         const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
+                         int dtype, void *c, const int *shape_c, int nd_c, size_t begin, size_t end)
 {
-    if (dtype != OR_F32 && dtype != OR_F16 && dtype != OR_BF16)
-        return OR_EINVAL;
-    if (nd_a < 2 || nd_b < 2 || nd_c < 2 || shape_a[nd_a - 1] != shape_b[nd_b - 2])
-        return OR_EINVAL;
     size_t rows = (size_t)shape_c[nd_c - 2], cols = (size_t)shape_c[nd_c - 1];
-    size_t total = shape_elements(shape_c, nd_c);
     int inner = shape_a[nd_a - 1];
-    for (size_t i = 0; i < total; i++) {
+    for (size_t i = begin; i < end; i++) {
         size_t batch = i / cols / rows;
         size_t oa = batch_offset(shape_a, strides_a, nd_a, batch, shape_c, nd_c) +
             (i / cols % rows) * strides_a[nd_a - 2];
@@ -570,6 +568,80 @@ int or_matmul(const void *a, const int *shape_a, const size_t *strides_a, int nd
         }
         store_ld(c, dtype, i, sum);
     }
+}
+
+int or_matmul(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
+              const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
+              int dtype, void *c, const int *shape_c, int nd_c)
+{
+    if (dtype != OR_F32 && dtype != OR_F16 && dtype != OR_BF16)
+        return OR_EINVAL;
+    if (nd_a < 2 || nd_b < 2 || nd_c < 2 || shape_a[nd_a - 1] != shape_b[nd_b - 2])
+        return OR_EINVAL;
+    matmul_range(a, shape_a, strides_a, nd_a, b, shape_b, strides_b, nd_b, dtype, c, shape_c, nd_c, 0,
+                 shape_elements(shape_c, nd_c));
+    return OR_OK;
+}
+
+struct matmul_job {
+    const void *a, *b;
+    const int *shape_a, *shape_b, *shape_c;
+    const size_t *strides_a, *strides_b;
+    int nd_a, nd_b, nd_c, dtype;
+    void *c;
+    size_t begin, end;
+};
+
+static void *matmul_worker(void *arg)
+{
+    const struct matmul_job *j = arg;
+    matmul_range(j->a, j->shape_a, j->strides_a, j->nd_a, j->b, j->shape_b, j->strides_b, j->nd_b, j->dtype, j->c,
+                 j->shape_c, j->nd_c, j->begin, j->end);
+    return NULL;
+}
+
+int or_matmul_mt(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
+                 const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
+                 int dtype, void *c, const int *shape_c, int nd_c, int threads)
+{
+    if (dtype != OR_F32 && dtype != OR_F16 && dtype != OR_BF16)
+        return OR_EINVAL;
+    if (nd_a < 2 || nd_b < 2 || nd_c < 2 || shape_a[nd_a - 1] != shape_b[nd_b - 2])
+        return OR_EINVAL;
+    if (threads < 1 || threads > 256)
+        return OR_EINVAL;
+    size_t total = shape_elements(shape_c, nd_c);
+    pthread_t tid[256];
+    int running[256] = {0};
+    struct matmul_job jobs[256];
+    for (int t = 0; t < threads; t++) {
+        struct matmul_job *j = &jobs[t];
+        j->a = a;
+        j->b = b;
+        j->shape_a = shape_a;
+        j->shape_b = shape_b;
+        j->shape_c = shape_c;
+        j->strides_a = strides_a;
+        j->strides_b = strides_b;
+        j->nd_a = nd_a;
+        j->nd_b = nd_b;
+        j->nd_c = nd_c;
+        j->dtype = dtype;
+        j->c = c;
+        j->begin = total * (size_t)t / (size_t)threads;
+        j->end = total * (size_t)(t + 1) / (size_t)threads;
+    }
+    /* ranges 1.. on their own threads (or here, when a thread cannot start),
+     * range 0 on the caller's thread */
+    for (int t = 1; t < threads; t++) {
+        if (pthread_create(&tid[t], NULL, matmul_worker, &jobs[t]) == 0)
+            running[t] = 1;
+        else
+            matmul_worker(&jobs[t]);
+    }
+    matmul_worker(&jobs[0]);
+    for (int t = 1; t < threads; t++)
+        if (running[t]) pthread_join(tid[t], NULL);
     return OR_OK;
 }
 

@@ -120,6 +120,11 @@ int or_layernorm_f32(const float *x, size_t rows, size_t n, float eps,
 int or_matmul(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
               const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
               int dtype, void *c, const int *shape_c, int nd_c);
+/* or_matmul with its outputs split over `threads` host threads (1..256): the
+ * same per-output sum, so the same bits. */
+int or_matmul_mt(const void *a, const int *shape_a, const size_t *strides_a, int nd_a,
+                 const void *b, const int *shape_b, const size_t *strides_b, int nd_b,
+                 int dtype, void *c, const int *shape_c, int nd_c, int threads);
 
 /* ---- HostArray binary arithmetic: contiguous_array_ce.c:1345-1447 -------
  * Floating dtypes only (f32/f64/f16/bf16), broadcast shapes, contiguous

@@ -223,9 +223,10 @@ def matmul_shape(sa, sb):
     return tuple(batch) + (sa[-2], sb[-1])
 
 
-def matmul(a, b, dtype, strides_a=None, strides_b=None, shape_a=None, shape_b=None):
+def matmul(a, b, dtype, strides_a=None, strides_b=None, shape_a=None, shape_b=None, threads=1):
     """HostArray matmul over storage arrays (optionally strided views given
-    as a base buffer plus element strides)."""
+    as a base buffer plus element strides); threads > 1 splits the outputs
+    over host threads (or_matmul_mt: the same per-output sums)."""
     shape_a = tuple(shape_a if shape_a is not None else a.shape)
     shape_b = tuple(shape_b if shape_b is not None else b.shape)
     if strides_a is None:
@@ -236,6 +237,11 @@ def matmul(a, b, dtype, strides_a=None, strides_b=None, shape_a=None, shape_b=No
         strides_b = [s // b.itemsize for s in b.strides]
     shape_c = matmul_shape(shape_a, shape_b)
     c = np.zeros(shape_c, NP_STORAGE[dtype])
+    if threads > 1:
+        _check(lib().or_matmul_mt(_p(a), _ints(shape_a), _sizes(strides_a), len(shape_a),
+                                  _p(b), _ints(shape_b), _sizes(strides_b), len(shape_b),
+                                  dtype, _p(c), _ints(shape_c), len(shape_c), int(threads)), "matmul")
+        return c
     _check(lib().or_matmul(_p(a), _ints(shape_a), _sizes(strides_a), len(shape_a),
                            _p(b), _ints(shape_b), _sizes(strides_b), len(shape_b),
                            dtype, _p(c), _ints(shape_c), len(shape_c)), "matmul")

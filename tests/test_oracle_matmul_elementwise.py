@@ -34,6 +34,26 @@ def test_matmul_reference_vectors(case):
         assert vals.tolist() == [float(v) for v in case["expected"]]
 
 
+@pytest.mark.parametrize("threads", [2, 3, 8])
+def test_threaded_matmul_gives_the_same_bits(threads):
+    """or_matmul_mt (the bench's CPU baseline driver) splits the outputs over
+    host threads; every output keeps or_matmul's sum, so the bits agree, for
+    batch broadcasting, a strided (transposed) operand and 16-bit outputs,
+    and for output counts that do not divide evenly."""
+    rng = np.random.default_rng(threads)
+    a = rng.standard_normal((3, 37, 51)).astype(np.float32)
+    b = rng.standard_normal((1, 51, 29)).astype(np.float32)
+    assert O.matmul(a, b, O.F32, threads=threads).tobytes() == O.matmul(a, b, O.F32).tobytes()
+    base = rng.standard_normal((51, 37)).astype(np.float32)  # A = base^T as a view
+    kw = dict(strides_a=[1, 37], shape_a=[37, 51])
+    b2 = rng.standard_normal((51, 29)).astype(np.float32)
+    assert (O.matmul(base, b2, O.F32, threads=threads, **kw).tobytes() ==
+            O.matmul(base, b2, O.F32, **kw).tobytes())
+    for dt in (O.BF16, O.F16):
+        a16, b16 = O.to_storage(a.astype(np.float64), dt), O.to_storage(b.astype(np.float64), dt)
+        assert O.matmul(a16, b16, dt, threads=threads).tobytes() == O.matmul(a16, b16, dt).tobytes()
+
+
 def test_matmul_transposed_view_integer_pattern():
     # ca_matmul_accelerated.phpt:31-48: left^T @ right with exact integers
     rows, cols = np.meshgrid(np.arange(64), np.arange(128), indexing="ij")
