@@ -519,6 +519,60 @@ __device__ __forceinline__ void store_row(OS *y, int n, int wr, int lane, bool f
     }
 }
 
+// Argmax / argmin of fp32 rows held in registers, in two passes over the
+// registers: the row's best value as the max (min) reduction computes it
+// (fmaxf / fminf: a NaN is never taken), then the lowest index holding
+// that value (each lane scans its elements from the highest index down, so
+// its last hit is its lowest; lanes and waves keep the minimum).  The result
+// is ArgAcc's: ties go to the lowest index, ±0 compare equal, and a row
+// whose best is the identity (every element -inf for argmax, +inf for
+// argmin, or NaN) gives index 0, since ArgAcc's strict comparison never
+// takes such an element.  Per element this is one max and one compare-select
+// against ArgAcc's compare and two selects.
+template <int VEC, int NCH, int WPR, bool MAXIMIZE>
+__global__ __launch_bounds__(64 * RowShape<WPR>::BW) void k_row_arg2(const void *__restrict__ xin, size_t rows,
+                                                                      int n, size_t ld, void *__restrict__ out)
+{
+    static_assert(WPR > 1, "one row per block");
+    constexpr int BW = RowShape<WPR>::BW;
+    __shared__ float lds_v[BW];
+    __shared__ int lds_i[BW];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, wr = wave;
+    const size_t row = blockIdx.x;
+    if (row >= rows) return;  // whole block
+    const float *x = (const float *)xin + row * ld;
+    const float ident = MAXIMIZE ? -INFINITY : INFINITY;
+    float v[NCH][VEC];
+    load_row<PT_FLOAT32, VEC, NCH, WPR, true>(x, n, wr, lane, ident, v);
+    auto best = [](float a, float b) { return MAXIMIZE ? fmaxf(a, b) : fminf(a, b); };
+    float m = ident;
+#pragma unroll
+    for (int c = 0; c < NCH; c++)
+#pragma unroll
+        for (int k = 0; k < VEC; k++) m = best(m, v[c][k]);
+    m = wave_all(m, best);
+    if (lane == 0) lds_v[wave] = m;
+    __syncthreads();
+    m = lds_v[0];
+#pragma unroll
+    for (int w = 1; w < WPR; w++) m = best(m, lds_v[w]);
+    // lowest index holding m (elements past n hold the identity: they can
+    // match only when m is the identity, whose result is 0 anyway)
+    int idx = 0x7fffffff;
+#pragma unroll
+    for (int c = NCH - 1; c >= 0; c--)
+#pragma unroll
+        for (int k = VEC - 1; k >= 0; k--)
+            if (v[c][k] == m) idx = chunk_start<VEC, WPR>(c, wr, lane) + k;
+    idx = wave_all(idx, [](int a, int b) { return a < b ? a : b; });
+    if (lane == 0) lds_i[wave] = idx;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    for (int w = 1; w < WPR; w++) idx = min(idx, lds_i[w]);
+    ((int32_t *)out)[row] = m == ident ? 0 : idx;
+}
+
 // Variance / standard deviation: exact two-pass form (mean, then the sum of
 // squared deviations from it) over the values held in registers.  Same
 // result definition as the Welford kernels (M2 / (n - correction), sqrt for
@@ -1537,23 +1591,24 @@ static bool as_rows(const int *shape, const size_t *strides, int ndims, int axis
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Waves per row of the block-per-row kernels on fp32 rows of 5 to 16
-// chunks of 16 bytes per wave-row step (up to 4096 floats): 8 for sum /
-// mean / max / min / prod, variance, softmax and layerNorm, 4 for argmax /
-// argmin.  On config 2 (X[8192, 4096]) against 4 waves: sum 20.5 against
-// 20.8 us, softmax 41.6 against 42.9 us, layerNorm 43.4 against 43.9 us,
-// variance (single-exchange Chan merge) 20.9-21.0 against 21.1; argmax took
-// 22.8 against 21.3 us.  16 waves (1024-thread blocks) ran 30-60 % slower for every op,
-// and nontemporal row loads or stores slowed softmax and layerNorm at every
-// width.  PT_ROW_WAVES (4 or 8) overrides the choice, a tuning knob read
-// once from the environment.
-static int row_waves(bool arg)
+// chunks of 16 bytes per wave-row step (up to 4096 floats): 8 for every op.
+// On config 2 (X[8192, 4096]) against 4 waves: sum 20.5 against 20.8 us,
+// softmax 41.6 against 42.9 us, layerNorm 43.4 against 43.9 us, variance
+// (single-exchange Chan merge) 20.9-21.0 against 21.1; argmax / argmin with
+// the two-pass k_row_arg2 20.4-20.5 against 21.3-21.4 us for the 4-wave
+// (value, index) kernel (8 waves of that kernel took 22.8 us).  16 waves
+// (1024-thread blocks) ran 30-60 % slower for every op, and nontemporal row
+// loads or stores slowed softmax and layerNorm at every width.  PT_ROW_WAVES
+// (4 or 8) overrides the choice, a tuning knob read once from the
+// environment.
+static int row_waves()
 {
     static const int w = [] {
         const char *e = getenv("PT_ROW_WAVES");
         const int v = e && *e ? atoi(e) : 0;
-        return (v == 4 || v == 8) ? v : 0;
+        return (v == 4 || v == 8) ? v : 8;
     }();
-    return w ? w : arg ? 4 : 8;
+    return w;
 }
 
 template <int DT, int OP>
@@ -1564,11 +1619,13 @@ static void launch_rows_t(const void *x, size_t rows, int n, size_t ld, void *ou
     dim3 block(256);
     if constexpr (DT == PT_FLOAT32) {
         const int chunks = (n + 64 * V - 1) / (64 * V);
-        if (row_waves(OP == R_ARGMAX || OP == R_ARGMIN) == 8 && n % V == 0 && ld % V == 0 && aligned16(x) &&
+        if (row_waves() == 8 && n % V == 0 && ld % V == 0 && aligned16(x) &&
             chunks > 4 && chunks <= 16) {
             dim3 grid1((unsigned)rows), block8(512);
             if constexpr (OP == R_VAR)
                 k_row_moments<DT, V, 2, 8><<<grid1, block8, 0, s>>>(x, rows, n, ld, out, out_dt, correction, take_sqrt);
+            else if constexpr (OP == R_ARGMAX || OP == R_ARGMIN)
+                k_row_arg2<V, 2, 8, OP == R_ARGMAX><<<grid1, block8, 0, s>>>(x, rows, n, ld, out);
             else
                 k_row_reduce<DT, OP, V, 8><<<grid1, block8, 0, s>>>(x, rows, n, ld, out, out_dt, 0, 0);
             return;
@@ -1859,7 +1916,7 @@ static void launch_softmax_rows(const void *x, size_t rows, int n, size_t ld, OS
     bool vec = n % V == 0 && ld % V == 0 && aligned16(x) && aligned16(y);
     int chunks = (n + 64 * V - 1) / (64 * V);
     if constexpr (DT == PT_FLOAT32) {
-        if (vec && chunks > 4 && chunks <= 16 && row_waves(false) == 8) {
+        if (vec && chunks > 4 && chunks <= 16 && row_waves() == 8) {
             k_row_softmax<DT, V, 2, 8, OS><<<grid1, dim3(512), 0, s>>>(x, rows, n, ld, y);
             return;
         }
@@ -1915,7 +1972,7 @@ static void launch_layernorm_rows(const void *x, size_t rows, int n, CT eps, con
                (!b || aligned16(b));
     int chunks = (n + 64 * V - 1) / (64 * V);
     if constexpr (DT == PT_FLOAT32 && sizeof(CT) == 4) {
-        if (vec && chunks > 4 && chunks <= 16 && row_waves(false) == 8) {
+        if (vec && chunks > 4 && chunks <= 16 && row_waves() == 8) {
             constexpr auto k = k_row_layernorm<DT, V, 2, 8, CT>;
             k<<<walk_grid<k, 512>(rows), dim3(512), 0, s>>>(x, rows, n, eps, g, b, y);
             return;

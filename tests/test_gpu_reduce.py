@@ -125,7 +125,7 @@ def test_arg_reduce_f32_vs_oracle(G, shape, op):
         assert np.array_equal(got, ref)
 
 
-@pytest.mark.parametrize("reps", [300, 1100])
+@pytest.mark.parametrize("reps", [300, 1024, 1100])
 def test_argmax_nan_inf_rules(G, reps):
     inf, nan = np.inf, np.nan
     x = np.array([[nan, 1.0, 3.0, 3.0], [-inf, -inf, -inf, -inf], [nan] * 4,
