@@ -484,7 +484,10 @@ _MLP_GEMMS = {
 def mlp_gemms(steps):
     """The five large fp32 products of the config-5 step, each timed alone
     (graph replays of pt_matmul on synthetic operands of the step's shapes
-    and layouts)."""
+    and layouts).  Split-K scratch comes from a workspace sized by one
+    measuring call and handed in with pt_workspace_begin, as the compiled
+    plan hands it to its native steps, so the graph holds no allocation
+    nodes."""
     lib = A.load()
     rng = np.random.default_rng(5)
     out = {}
@@ -497,8 +500,21 @@ def mlp_gemms(steps):
         m, k, n = ash[0], ash[1], bsh[1]
         sa, sta, sb, stb, sc = A.ints(list(ash)), A.sizes(list(ast)), A.ints(list(bsh)), A.sizes(list(bst)), A.ints([m, n])
 
-        def launch(stream, r, da=da, db=db, sa=sa, sta=sta, sb=sb, stb=stb, sc=sc):
+        def matmul(stream, da=da, db=db, sa=sa, sta=sta, sb=sb, stb=stb, sc=sc):
             A.check(lib.pt_matmul(da.ptr, db.ptr, c.ptr, A.FLOAT32, sa, sta, 2, sb, stb, 2, sc, 2, stream), "matmul")
+        A.check(lib.pt_workspace_begin(None, 0), "workspace")
+        matmul(None)
+        peak = ctypes.c_size_t()
+        A.check(lib.pt_workspace_end(ctypes.byref(peak)), "workspace")
+        ws_bytes = max(256, peak.value)
+        ws = A.DeviceBuffer(ws_bytes)
+
+        def launch(stream, r, matmul=matmul, ws=ws, ws_bytes=ws_bytes):
+            A.check(lib.pt_workspace_begin(ws.ptr, ws_bytes), "workspace")
+            try:
+                matmul(stream)
+            finally:
+                A.check(lib.pt_workspace_end(None), "workspace")
         t = GraphTimer(launch, reps=4)
         warm_up(t.run, 2, t.reps)
         ms = t.run(max(2, steps))
