@@ -54,7 +54,8 @@ PMC_TRAFFIC_BYTES = {
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol
 GEMM_KERNELS = {"mfma-lds-wholeline": "k_gemm_wl", "mfma-lds-pingpong": "k_gemm_pp", "mfma-lds-ring": "k_gemm_ring",
-                "mfma-direct-lds": "k_gemm_direct", "mfma-fp32": "k_gemm", "mfma-low-precision": "k_gemm"}
+                "mfma-direct-lds": "k_gemm_direct", "mfma-fp32": "k_gemm", "mfma-low-precision": "k_gemm",
+                "mfma-fp32-ring": "k_gemm_f32r"}
 MALL_BYTES = 256 << 20
 
 

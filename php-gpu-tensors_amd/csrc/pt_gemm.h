@@ -1,4 +1,5 @@
-// Internal header of the GEMM kernels (pt_gemm.hip, pt_gemm_ring.hip):
+// Internal header of the GEMM kernels (pt_gemm.hip, pt_gemm_ring.hip,
+// pt_gemm_f32ring.hip, pt_gemm_smalln.hip):
 // argument block, element traits, MFMA fragment types and helpers shared by
 // the kernels.  Not part of the public boundary (include/pt_hip.h is).
 #pragma once
@@ -99,6 +100,60 @@ __device__ __forceinline__ int swz_k(int row, int cpr)
     return cpr == 8 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 
+// ---- helpers of the LDS-ring kernels (pt_gemm_ring.hip, pt_gemm_f32ring.hip)
+template <int I> struct IC { static constexpr int value = I; };
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f)
+{
+    if constexpr (B < E) {
+        f(IC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
+// Wait until at most VM vector-memory operations of this wave are in
+// flight and all of its LDS reads have returned (gfx9 s_waitcnt fields:
+// vmcnt[3:0] bits 3:0, expcnt 6:4, lgkmcnt 11:8, vmcnt[5:4] 15:14).
+template <int VM>
+__device__ __forceinline__ void ring_wait()
+{
+    static_assert(VM >= 0 && VM < 64, "vmcnt range");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (0 << 8) | ((VM >> 4) << 14));
+}
+
+// Workgroup barrier without the memory-model fence of __syncthreads (which
+// would wait for every load in flight); the waits that make LDS data
+// visible are the explicit ring_wait before it.
+__device__ __forceinline__ void ring_barrier()
+{
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// LDS reads issued as inline asm (instruction offset OFF bytes).
+template <int OFF, typename T>
+__device__ __forceinline__ void lds_read_b128(T &dst, uint32_t addr)
+{
+    static_assert(sizeof(T) == 16 && OFF >= 0 && OFF < 65536, "ds_read_b128 operand");
+    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
+}
+typedef float f32x2v_t __attribute__((ext_vector_type(2)));
+template <int OFF>
+__device__ __forceinline__ void lds_read_b64(f32x2v_t &dst, uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read_b64 offset");
+    asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
+}
+template <int OFF>
+__device__ __forceinline__ void lds_read_tr16(s16x4_t &dst, uint32_t addr)
+{
+    static_assert(OFF >= 0 && OFF < 65536, "ds_read_b64_tr_b16 offset");
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
+}
+
 // LDS-ring kernels for 16-bit operands (pt_gemm_ring.hip).  A variant is a
 // (K step, stages, tile width, workgroups per CU, schedule, waves, kind)
 // shape; every variant needs M % 256 == 0, N % tile width == 0 and K a
@@ -110,6 +165,11 @@ int gemm_ring_bn(int variant);
 int gemm_ring_bk(int variant);
 int gemm_ring_kmul(int variant);
 void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s);
+
+// fp32 LDS-ring kernel for 128x128 tiles (pt_gemm_f32ring.hip); a_kc / b_kc:
+// the operand's K index is its contiguous one (else M / N is).
+bool gemm_f32r_eligible(const GemmArgs &g, bool a_kc, bool b_kc);
+void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, hipStream_t s);
 
 // fp32 products with N <= 16 and k-contiguous A (pt_gemm_smalln.hip).
 bool gemm_smalln_eligible(const GemmArgs &g);

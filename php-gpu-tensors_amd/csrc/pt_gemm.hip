@@ -744,7 +744,10 @@ enum GemmTile {
     // LDS-ring kernels (k_gemm_ring, k_gemm_pp, k_gemm_wl): variants 0..23
     // of gemm_ring_variants()
     TILE_RING_FIRST = 14, TILE_RING_LAST = 37,
-    TILE_COUNT = 38,
+    // fp32 LDS-ring kernel (k_gemm_f32r, pt_gemm_f32ring.hip): 128x128
+    // tiles, K steps of 32, one workgroup per CU
+    TILE_F32_RING = 38,
+    TILE_COUNT = 39,
     // large bf16 and fp16 products with K a multiple of 64: k_gemm_wl (the
     // 8-wave ring with A in whole 128-byte lines).  Config 4 at steady state,
     // alternating runs on one box: bf16 472-475 us against 488-490 us for the
@@ -761,7 +764,7 @@ static const TileInfo kTiles[TILE_COUNT] = {
     {256, 256, 1}, {256, 128, 1}, {256, 128, 1}, {256, 256, 2}, {256, 256, 1}, {256, 128, 1},
     {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1},
     {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1}, {256, 256, 1},
-    {256, 256, 1}, {256, 256, 1}};
+    {256, 256, 1}, {256, 256, 1}, {128, 128, 2}};
 
 static int g_tile_override = -1;
 
@@ -773,6 +776,19 @@ static long long splitk_workgroups()
         const char *e = getenv("PT_SPLITK_WORKGROUPS");
         const long long v = e && *e ? atoll(e) : 0;
         return v >= 64 && v <= 8192 ? v : 512;
+    }();
+    return w;
+}
+
+// The fp32 ring kernel holds a CU per workgroup (128 KiB of LDS): its K
+// split aims for one round of workgroups.  PT_SPLITK_RING_WORKGROUPS
+// overrides the target.
+static long long splitk_ring_workgroups()
+{
+    static const long long w = [] {
+        const char *e = getenv("PT_SPLITK_RING_WORKGROUPS");
+        const long long v = e && *e ? atoll(e) : 0;
+        return v >= 64 && v <= 8192 ? v : 256;
     }();
     return w;
 }
@@ -832,6 +848,17 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
         break;
     case TILE_128x64_W4M2_K2:
         if constexpr (DT == PT_FLOAT32) launch_layouts<DT, 128, 64, 2 * BK, 2, 2, 2>(g, a_kc, b_kc, check, s);
+        break;
+    case TILE_F32_RING:
+        // fp32 operands in 16-byte packs with whole K steps run the ring
+        // kernel (edge tiles included); others the 8-wave 128x128 kernel
+        if constexpr (DT == PT_FLOAT32) {
+            if (gemm_f32r_eligible(g, a_kc, b_kc)) {
+                launch_gemm_f32r(g, a_kc, b_kc, s);
+                break;
+            }
+        }
+        launch_layouts<DT, 128, 128, BK, 2, 4>(g, a_kc, b_kc, check, s);
         break;
     default: launch_layouts<DT, 64, 64, BK, 2, 2>(g, a_kc, b_kc, check, s); break;
     }
@@ -991,7 +1018,8 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
                                                 : TILE_64x64;
     }
     // the fp32-only tiles run the 128x128 kernel for 16-bit operands
-    if (dtype != PT_FLOAT32 && (tile == TILE_128x128_W8_K2 || tile == TILE_128x64_W4M2 || tile == TILE_128x64_W4M2_K2))
+    if (dtype != PT_FLOAT32 && (tile == TILE_128x128_W8_K2 || tile == TILE_128x64_W4M2 || tile == TILE_128x64_W4M2_K2 ||
+                                tile == TILE_F32_RING))
         tile = TILE_128x128;
     auto aligned = [](const void *p) { return ((uintptr_t)p & 15u) == 0; };
     if (tile >= TILE_RING_FIRST && tile <= TILE_RING_LAST) {
@@ -1054,19 +1082,6 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         }
         tile = TILE_256x256;
     }
-    int bm = kTiles[tile].bm, bn = kTiles[tile].bn;
-    const int BK = (dtype == PT_FLOAT32 ? 16 : 32) * kTiles[tile].kmul;
-    bool vec_ok = aligned(a) && aligned(b);
-    // vector (unchecked) loads need whole tiles, 16-byte aligned rows and
-    // batch offsets that keep that alignment
-    bool check = !(g.M % bm == 0 && g.N % bn == 0 && g.K % BK == 0 && vec_ok);
-    if (!check) {
-        long long lda = a_kc ? g.a_sm : g.a_sk, ldb = b_kc ? g.b_sn : g.b_sk;
-        if ((a_kc ? g.a_sk : g.a_sm) != 1 || (b_kc ? g.b_sk : g.b_sn) != 1) check = true;
-        if (lda % PKe || ldb % PKe) check = true;
-        for (int d = 0; d < g.nbd; d++)
-            if (g.bsa[d] % PKe || g.bsb[d] % PKe) check = true;
-    }
     // checked kernels still load whole 16-byte packs that lie inside the
     // matrix when the operand's contiguous stride is 1 and its pitch and
     // batch offsets keep packs aligned
@@ -1080,6 +1095,29 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         g.vec_a = va;
         g.vec_b = vb;
     }
+    // fp32 products of 128 x 128 tiles or more run the ring kernel wherever
+    // it takes the operands (16-byte packs, whole 32-k steps); the others
+    // keep the 256x256 or 8-wave 128x128 tiles chosen above.  Config 4 fp32
+    // at steady state: 3711-3721 us against 3913 us (256x256); the config-5
+    // products: G2 64.1 us against 73.3 us, dW2 69.8 against 78.0 us.
+    if (dtype == PT_FLOAT32 && g_tile_override < 0 && !tuned && (tile == TILE_256x256 || tile == TILE_128x128_W8)) {
+        GemmArgs whole = g;
+        whole.ksplit = 1;
+        if (gemm_f32r_eligible(whole, a_kc, b_kc)) tile = TILE_F32_RING;
+    }
+    int bm = kTiles[tile].bm, bn = kTiles[tile].bn;
+    const int BK = (dtype == PT_FLOAT32 ? 16 : 32) * kTiles[tile].kmul;
+    bool vec_ok = aligned(a) && aligned(b);
+    // vector (unchecked) loads need whole tiles, 16-byte aligned rows and
+    // batch offsets that keep that alignment
+    bool check = !(g.M % bm == 0 && g.N % bn == 0 && g.K % BK == 0 && vec_ok);
+    if (!check) {
+        long long lda = a_kc ? g.a_sm : g.a_sk, ldb = b_kc ? g.b_sn : g.b_sk;
+        if ((a_kc ? g.a_sk : g.a_sm) != 1 || (b_kc ? g.b_sk : g.b_sn) != 1) check = true;
+        if (lda % PKe || ldb % PKe) check = true;
+        for (int d = 0; d < g.nbd; d++)
+            if (g.bsa[d] % PKe || g.bsb[d] % PKe) check = true;
+    }
     long long total_tiles = (long long)((g.M + bm - 1) / bm) * ((g.N + bn - 1) / bn) * batch;
     g.remap = total_tiles % 8 == 0;
     if (total_tiles > 0x7fffffffLL) return fail(PT_ERR_INVALID, "matmul grid too large");
@@ -1091,7 +1129,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
     g.partial = nullptr;
     if (total_tiles < 256 && g.K >= 8 * BK) {
         // whole rounds: about 2 workgroups per CU, never a partial second round
-        long long want = splitk_workgroups() / total_tiles;
+        long long want = (tile == TILE_F32_RING ? splitk_ring_workgroups() : splitk_workgroups()) / total_tiles;
         long long max_split = g.K / (4 * BK);
         int ks = (int)(want < max_split ? want : max_split);
         if (ks > 64) ks = 64;
@@ -1107,6 +1145,7 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
             }
         }
     }
+    const bool f32ring = dtype == PT_FLOAT32 && tile == TILE_F32_RING && gemm_f32r_eligible(g, a_kc, b_kc);
     switch (dtype) {
     case PT_BFLOAT16: launch_dt<PT_BFLOAT16>(g, tile, a_kc, b_kc, check, s); break;
     case PT_FLOAT16: launch_dt<PT_FLOAT16>(g, tile, a_kc, b_kc, check, s); break;
@@ -1135,13 +1174,14 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         PT_TRY(check_hip(e2, "matmul (split-K sum)"));
         counters().mfma_gemm_calls++;
         snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s%s",
-                 dtype == PT_FLOAT32 ? "mfma-fp32-splitk" : "mfma-low-precision-splitk", suffix);
+                 f32ring ? "mfma-fp32-ring-splitk" : dtype == PT_FLOAT32 ? "mfma-fp32-splitk" : "mfma-low-precision-splitk",
+                 suffix);
         return PT_OK;
     }
     PT_LAUNCH_CHECK("matmul");
     counters().mfma_gemm_calls++;
     snprintf(counters().last_matmul, sizeof(counters().last_matmul), "%s%s",
-             dtype == PT_FLOAT32 ? "mfma-fp32" : "mfma-low-precision", suffix);
+             f32ring ? "mfma-fp32-ring" : dtype == PT_FLOAT32 ? "mfma-fp32" : "mfma-low-precision", suffix);
     return PT_OK;
 }
 
@@ -1164,7 +1204,7 @@ pt_status pt_matmul_tune(const void *a, const void *b, void *c, int dtype,
     const bool a_k1 = strides_a[nd_a - 1] == 1, b_k1 = strides_b[nd_b - 2] == 1;
     static const int kFp32[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
                                 TILE_256x128_W8, TILE_128x128_W8, TILE_128x128_W8_K2, TILE_128x64_W4M2,
-                                TILE_128x64_W4M2_K2};
+                                TILE_128x64_W4M2_K2, TILE_F32_RING};
     static const int kHalf[] = {TILE_256x128, TILE_128x128, TILE_64x64, TILE_256x256, TILE_256x256_K2,
                                 TILE_256x256_DIRECT, TILE_256x128_W8, TILE_128x128_W8, TILE_RING_DEFAULT,
                                 TILE_RING_HALF, TILE_RING_FIRST + 12, TILE_RING_FIRST + 7, TILE_RING_FIRST + 15};

@@ -30,52 +30,6 @@ namespace pt {
 // Loads thus have NST-1 steps to land.  Loads past the last step re-read
 // the last K step (in bounds, never consumed), so every step waits for the
 // same count.
-template <int I> struct IC { static constexpr int value = I; };
-template <int B, int E, typename F>
-__device__ __forceinline__ void static_for(F &&f)
-{
-    if constexpr (B < E) {
-        f(IC<B>{});
-        static_for<B + 1, E>(f);
-    }
-}
-
-// Wait until at most VM vector-memory operations of this wave are in
-// flight and all of its LDS reads have returned (gfx9 s_waitcnt fields:
-// vmcnt[3:0] bits 3:0, expcnt 6:4, lgkmcnt 11:8, vmcnt[5:4] 15:14).
-template <int VM>
-__device__ __forceinline__ void ring_wait()
-{
-    static_assert(VM >= 0 && VM < 64, "vmcnt range");
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | (0 << 8) | ((VM >> 4) << 14));
-}
-
-// Workgroup barrier without the memory-model fence of __syncthreads (which
-// would wait for every load in flight); the waits that make LDS data
-// visible are the explicit ring_wait before it.
-__device__ __forceinline__ void ring_barrier()
-{
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// LDS reads issued as inline asm (instruction offset OFF bytes).
-template <int OFF, typename T>
-__device__ __forceinline__ void lds_read_b128(T &dst, uint32_t addr)
-{
-    static_assert(sizeof(T) == 16 && OFF >= 0 && OFF < 65536, "ds_read_b128 operand");
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
-}
-template <int OFF>
-__device__ __forceinline__ void lds_read_tr16(s16x4_t &dst, uint32_t addr)
-{
-    static_assert(OFF >= 0 && OFF < 65536, "ds_read_b64_tr_b16 offset");
-    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
-}
-
 // Two fp32 values rounded to the 16-bit dtype, packed low | high << 16.
 // bf16: v_cvt_pk_bf16_f32 rounds to nearest even and quiets NaN exactly as
 // float_to_bf16 does (checked bit for bit over every exponent / top-mantissa

@@ -151,6 +151,62 @@ def test_matmul_split_k(A, bmnk, dt):
     assert np.all(np.abs(got - r) <= tol)
 
 
+def _ring_eligible(m, n, k, layout):
+    """The fp32 ring kernel's conditions (pt_gemm_f32ring.hip) for these
+    aligned, packed operands: whole K steps of 32, and a transposed (m- or
+    n-contiguous) operand needs its M or N a multiple of 4."""
+    a_rc, b_rc = layout[0] == "T", layout[1] == "N"
+    return k % 32 == 0 and (not a_rc or m % 4 == 0) and (not b_rc or n % 4 == 0)
+
+
+@pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
+@pytest.mark.parametrize("bmnk", [(2, 256, 384, 128), (1, 300, 260, 96), (1, 784, 1024, 4096),
+                                  (3, 130, 258, 64), (1, 128, 129, 32), (1, 1024, 1024, 2048),
+                                  (2, 256, 256, 130)], ids=str)
+def test_matmul_fp32_ring(A, bmnk, layout):
+    """Tile 38, the fp32 LDS-ring kernel: every operand layout (A k- or
+    m-contiguous, B n- or k-contiguous), whole and edge tiles (rows past M
+    and columns past N load clamped packs and are not stored), batches, and
+    split-K over long K with few tiles.  Integer-valued operands keep every
+    sum exact, so outputs are bit-exact against numpy's float64 product.
+    Shapes the kernel does not take (K % 32 != 0, a transposed operand whose
+    M or N is not a multiple of 4) run the 8-wave 128x128 kernel instead and
+    must agree too."""
+    from phptensors import synthetic
+    b_, m, n, k = bmnk
+    A.load().pt_matmul_set_tile(38)
+    try:
+        a = _ints((b_, m, k), seed=m + 3 * k, lo=-4, hi=4)
+        b = _ints((b_, k, n), seed=n + 5 * k, lo=-4, hi=4)
+        expect = (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+        kw = {}
+        a_in, b_in = a, b
+        if layout[0] == "T":   # A as the transposed view of a [b, k, m] buffer
+            a_in = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+            kw.update(shape_a=(b_, m, k), strides_a=[m * k, 1, m])
+        if layout[1] == "T":   # B as the transposed view of a [b, n, k] buffer
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+            kw.update(shape_b=(b_, k, n), strides_b=[n * k, 1, k])
+        assert np.array_equal(run(A, a_in, b_in, O.F32, **kw), expect)
+        path = A.backend_info().last_matmul.decode()
+        assert path.startswith("mfma-fp32-ring") == _ring_eligible(m, n, k, layout), path
+        if m * n * b_ <= 1024 * 1024 and k >= 2048:
+            assert path.endswith("splitk"), path
+        # random operands: the fp32 bar of the module docstring
+        a = synthetic.normal((b_, m, k), 0.0, 1.0, seed=k + 7).astype(np.float32)
+        b = synthetic.normal((b_, k, n), 0.0, 1.0, seed=k + 8).astype(np.float32)
+        a_in, b_in = a, b
+        if layout[0] == "T":
+            a_in = np.ascontiguousarray(np.swapaxes(a, 1, 2))
+        if layout[1] == "T":
+            b_in = np.ascontiguousarray(np.swapaxes(b, 1, 2))
+        got = run(A, a_in, b_in, O.F32, **kw).astype(np.float64)
+        a64, b64 = a.astype(np.float64), b.astype(np.float64)
+        assert np.all(np.abs(got - a64 @ b64) <= 1e-4 * math.sqrt(k) * (np.abs(a64) @ np.abs(b64)))
+    finally:
+        A.load().pt_matmul_set_tile(-1)
+
+
 @pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
 @pytest.mark.parametrize("bmnk", [(1, 512, 256, 512), (2, 256, 512, 128), (3, 256, 256, 64),
@@ -539,9 +595,10 @@ def test_matmul_tuning_reference():
 
 def test_matmul_large_dispatch_reference():
     """matmul_large_dispatch.phpt: a 4096x4096 fp32 product of ones is exact
-    (4096 everywhere) and runs the large-problem MFMA kernel."""
+    (4096 everywhere) and runs the large-problem strict-fp32 kernel, here the
+    fp32 LDS-ring MFMA kernel."""
     from phptensors import backend as B
     from phptensors import CudaArray
     out = CudaArray.ones([4096, 4096]).matmul(CudaArray.ones([4096, 4096])).toNumpy()
     assert np.all(out == 4096.0)
-    assert B.cuda_get_backend_info()["lastMatmul"] == "mfma-fp32"
+    assert B.cuda_get_backend_info()["lastMatmul"] == "mfma-fp32-ring"
