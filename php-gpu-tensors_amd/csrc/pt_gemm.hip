@@ -1031,9 +1031,11 @@ pt_status pt_matmul(const void *a, const void *b, void *c, int dtype,
         const int kmul = gemm_ring_kmul(variant), bn = gemm_ring_bn(variant);
         const bool b_row = g.b_sn == 1, b_col = g.b_sk == 1;
         const long long ldb = b_row ? g.b_sk : g.b_sn;
+        // (pitches below 2^22 elements: the whole-line kernel's per-lane
+        // byte offsets within a step are 32-bit)
         bool ok = dtype != PT_FLOAT32 && g.a_sk == 1 && (b_row || b_col) && g.M % 256 == 0 && g.N % bn == 0 &&
                   g.K % kmul == 0 && aligned(a) && aligned(b) && ((uintptr_t)c & 3u) == 0 && g.a_sm % 8 == 0 &&
-                  ldb % 8 == 0;
+                  ldb % 8 == 0 && g.a_sm <= (1LL << 22) && ldb <= (1LL << 22);
         for (int d = 0; d < g.nbd; d++)
             if (g.bsa[d] % 8 || g.bsb[d] % 8) ok = false;
         long long tiles = (long long)(g.M / 256) * (g.N / bn) * batch;

@@ -121,23 +121,15 @@ __global__ __launch_bounds__(256, 1) void k_gemm_f32r(GemmArgs g)
     const int KT = Kl / BK;
 
     // load IDX of step kt into stage J (loads past the last step re-read it:
-    // in bounds, never consumed, and every step waits for the same count).
-    // A buffer load to LDS: the step's base in a scalar resource (raw
-    // buffer, stride 0, no range limit), the lane's offset in a register.
+    // in bounds, never consumed, and every step waits for the same count)
     auto issue = [&](int kt, auto J, auto IDX) {
         constexpr int j = decltype(J)::value % NST, q = decltype(IDX)::value;
-        constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
         if constexpr (q < NQ) {
-            const __amdgpu_buffer_rsrc_t r =
-                __builtin_amdgcn_make_buffer_rsrc((void *)(A0 + (long long)kt * sta), (short)0, -1, kRsrcWord3);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (PT_LDS_AS void *)(lds_a + j * SE + (wave * NQ + q) * 256),
-                                                     16, offa[q], 0, 0, 0);
+            buffer_load_lds16(A0 + (long long)kt * sta, offa[q], (PT_LDS_AS void *)(lds_a + j * SE + (wave * NQ + q) * 256));
         } else {
             constexpr int q2 = q - NQ;
-            const __amdgpu_buffer_rsrc_t r =
-                __builtin_amdgcn_make_buffer_rsrc((void *)(B0 + (long long)kt * stb), (short)0, -1, kRsrcWord3);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (PT_LDS_AS void *)(lds_b + j * SE + (wave * NQ + q2) * 256),
-                                                     16, offb[q2], 0, 0, 0);
+            buffer_load_lds16(B0 + (long long)kt * stb, offb[q2],
+                              (PT_LDS_AS void *)(lds_b + j * SE + (wave * NQ + q2) * 256));
         }
     };
 

@@ -714,29 +714,35 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wl(GemmArgs g)
     const S *B = (const S *)g.b + ob + (B_KC ? (long long)n0 * g.b_sn : (long long)n0);
     const long long lda = g.a_sm, ldb = B_KC ? g.b_sn : g.b_sk;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    // the wave index as a uniform value (the loads' LDS destinations are
+    // scalar arithmetic)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
 
     // A load (half h, instruction q4 of the wave): rows h*128 + 8q .. +7,
-    // lane L at row 8q + L/8, LDS position L % 8 holding chunk (L%8) ^ swizzle
-    long long offa[2][NQA], offb[NQB];
+    // lane L at row 8q + L/8, LDS position L % 8 holding chunk (L%8) ^ swizzle.
+    // Offsets are the lane's bytes from the step's base (the host keeps the
+    // pitches below 2^22 elements, so they fit 32 bits): each load is one
+    // buffer load to LDS with a scalar base.
+    uint32_t offa[2][NQA], offb[NQB];
 #pragma unroll
     for (int h = 0; h < 2; h++)
 #pragma unroll
         for (int q4 = 0; q4 < NQA; q4++) {
             const int q = wave * NQA + q4;
             const int row = h * 128 + q * 8 + lane / 8, p = lane % 8;
-            offa[h][q4] = (long long)row * lda + ((p ^ swz_k(row, 8)) << 3);
+            offa[h][q4] = (uint32_t)(((long long)row * lda + ((p ^ swz_k(row, 8)) << 3)) * 2);
         }
 #pragma unroll
     for (int q4 = 0; q4 < NQB; q4++) {
         const int q = wave * NQB + q4;
         if constexpr (B_KC) {
             const int row = q * RPI + lane / CPR, pc = lane % CPR;
-            offb[q4] = (long long)row * ldb + (pc ^ swz_k(row, CPR)) * 8;
+            offb[q4] = (uint32_t)(((long long)row * ldb + (pc ^ swz_k(row, CPR)) * 8) * 2);
         } else {
             const int krow = q * KPI + lane / CPB, pcb = lane % CPB;
-            offb[q4] = (long long)krow * ldb + (pcb ^ ((krow & 3) << 2)) * 8;
+            offb[q4] = (uint32_t)(((long long)krow * ldb + (pcb ^ ((krow & 3) << 2)) * 8) * 2);
         }
     }
     const long long bstep = B_KC ? (long long)BK : (long long)BK * ldb;
@@ -749,15 +755,13 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wl(GemmArgs g)
         if constexpr (idx < NQA) {
             constexpr int h = j & 1, slot = ((j + 4) >> 1) % NSA;
             const int s = min((u + 4) >> 1, KS - 1);
-            __builtin_amdgcn_global_load_lds(
-                (const void *)(A + (long long)s * 2 * BK + offa[h][idx]),
-                (PT_LDS_AS void *)(lds_a + slot * SA_ELEMS + (h * 128 + (wave * NQA + idx) * 8) * 2 * BK), 16, 0, 0);
+            buffer_load_lds16(A + (long long)s * 2 * BK, offa[h][idx],
+                              (PT_LDS_AS void *)(lds_a + slot * SA_ELEMS + (h * 128 + (wave * NQA + idx) * 8) * 2 * BK));
         } else {
             constexpr int q4 = idx - NQA, slot = (j + 3) % NSB;
             const int kb = min(u + 3, KT - 1);
-            __builtin_amdgcn_global_load_lds((const void *)(B + (long long)kb * bstep + offb[q4]),
-                                             (PT_LDS_AS void *)(lds_b + slot * B_ELEMS + (wave * NQB + q4) * 512),
-                                             16, 0, 0);
+            buffer_load_lds16(B + (long long)kb * bstep, offb[q4],
+                              (PT_LDS_AS void *)(lds_b + slot * B_ELEMS + (wave * NQB + q4) * 512));
         }
     };
 
