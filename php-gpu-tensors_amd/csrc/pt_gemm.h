@@ -180,9 +180,10 @@ int gemm_ring_kmul(int variant);
 void launch_gemm_ring(const GemmArgs &g, int dtype, bool b_row, int variant, dim3 grid, hipStream_t s);
 
 // fp32 LDS-ring kernel for 128x128 tiles (pt_gemm_f32ring.hip); a_kc / b_kc:
-// the operand's K index is its contiguous one (else M / N is).
+// the operand's K index is its contiguous one (else M / N is).  stages: 4
+// (128 KiB of LDS, one workgroup per CU) or 2 (64 KiB, two per CU).
 bool gemm_f32r_eligible(const GemmArgs &g, bool a_kc, bool b_kc);
-void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, hipStream_t s);
+void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, int stages, hipStream_t s);
 
 // fp32 products with N <= 16 and k-contiguous A (pt_gemm_smalln.hip).
 bool gemm_smalln_eligible(const GemmArgs &g);

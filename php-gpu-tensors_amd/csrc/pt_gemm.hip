@@ -780,15 +780,29 @@ static long long splitk_workgroups()
     return w;
 }
 
-// The fp32 ring kernel holds a CU per workgroup (128 KiB of LDS): its K
-// split aims for one round of workgroups.  PT_SPLITK_RING_WORKGROUPS
-// overrides the target.
+// Ring depth of the fp32 ring kernel: 4 stages (one workgroup per CU) or 2
+// (two per CU), for products with and without a K split.
+// PT_F32R_STAGES and PT_F32R_SPLIT_STAGES override them (tuning knobs read
+// once from the environment).
+static int ring_stages(bool split)
+{
+    auto read = [](const char *name, int dflt) {
+        const char *e = getenv(name);
+        const int v = e && *e ? atoi(e) : 0;
+        return v == 2 || v == 4 ? v : dflt;
+    };
+    static const int whole = read("PT_F32R_STAGES", 4), parts = read("PT_F32R_SPLIT_STAGES", 4);
+    return split ? parts : whole;
+}
+
+// The ring kernel's K split aims for one round of workgroups: 256 with 4
+// stages (a CU each), 512 with 2.  PT_SPLITK_RING_WORKGROUPS overrides it.
 static long long splitk_ring_workgroups()
 {
     static const long long w = [] {
         const char *e = getenv("PT_SPLITK_RING_WORKGROUPS");
         const long long v = e && *e ? atoll(e) : 0;
-        return v >= 64 && v <= 8192 ? v : 256;
+        return v >= 64 && v <= 8192 ? v : (ring_stages(true) == 2 ? 512 : 256);
     }();
     return w;
 }
@@ -854,7 +868,7 @@ static void launch_dt(GemmArgs g, int tile, bool a_kc, bool b_kc, bool check, hi
         // kernel (edge tiles included); others the 8-wave 128x128 kernel
         if constexpr (DT == PT_FLOAT32) {
             if (gemm_f32r_eligible(g, a_kc, b_kc)) {
-                launch_gemm_f32r(g, a_kc, b_kc, s);
+                launch_gemm_f32r(g, a_kc, b_kc, ring_stages(g.ksplit > 1), s);
                 break;
             }
         }

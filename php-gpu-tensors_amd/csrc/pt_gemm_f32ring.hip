@@ -37,18 +37,24 @@ namespace pt {
 // k-row read of the other layout supplies one.  Both operands follow that
 // order, so every MFMA pairs A and B at the same k, and each output's sum
 // over K runs in one fixed order.
-// Per step a wave issues 8 loads of 1 KiB, spread over the first 48 of its
-// 64 MFMAs, into the stage that the previous step's barrier freed; at its
-// own barrier it waits only for the loads of the next step (issued three
-// steps before), so the loads have about three steps to land.  Fragments
-// of slice s + 1 are read while slice s runs on the matrix cores.
+// Per step a wave issues 8 loads of 1 KiB, the loads of step t + NST - 1,
+// into the stage that the previous step's barrier freed, and at its own
+// barrier waits only for the loads of step t + 1:
+//   * NST = 4 (128 KiB of LDS, one workgroup per CU): loads spread over the
+//     first 48 of the step's 64 MFMAs; steps t + 2 and t + 3 stay in flight
+//     at the barrier, so a load has more than two steps to land;
+//   * NST = 2 (64 KiB, two workgroups per CU): loads issued one per MFMA at
+//     the start of the step, all landed at its barrier; the other
+//     workgroup's waves keep the SIMD busy while these wait.
+// Fragments of slice s + 1 are read while slice s runs on the matrix cores.
 // Edge tiles: rows past M (columns past N) load the last whole row or
 // 16-byte pack instead and are not stored.  K steps must be whole (each K
 // chunk a multiple of 32).
-template <bool A_KC, bool B_KC>
-__global__ __launch_bounds__(256, 1) void k_gemm_f32r(GemmArgs g)
+template <bool A_KC, bool B_KC, int NST>
+__global__ __launch_bounds__(256, NST == 2 ? 2 : 1) void k_gemm_f32r(GemmArgs g)
 {
-    constexpr int BM = 128, BN = 128, BK = 32, NST = 4, NS = BK / 8;
+    constexpr int BM = 128, BN = 128, BK = 32, NS = BK / 8;
+    static_assert(NST == 2 || NST == 4, "ring depth");
     constexpr int SE = BM * BK;       // floats per operand stage (16 KiB)
     constexpr int NQ = SE / 256 / 4;  // 1 KiB loads per operand, wave and step
     constexpr int PER = 2 * NQ;       // loads per wave and step
@@ -225,9 +231,13 @@ __global__ __launch_bounds__(256, 1) void k_gemm_f32r(GemmArgs g)
                 if constexpr (s + 1 < NS) read_one(J, IC<s + 1>{}, IC<st ^ 1>{}, Q);
                 else read_one(IC<j + 1>{}, IC<0>{}, IC<st ^ 1>{}, Q);
             }
+            // loads of step kt + NST - 1: spread over slices 0-2 in the
+            // 4-stage ring; in the 2-stage ring, one per MFMA at the start of
+            // the step, so that they have most of the step to land
             constexpr int slot = s * 16 + q;
-            if constexpr (s < NS - 1 && slot % 6 == 2 && slot / 6 < PER)
-                issue(min(kt + NST - 1, KT - 1), IC<j + NST - 1>{}, IC<slot / 6>{});
+            constexpr int SP = NST > 2 ? 6 : 1, OFF = NST > 2 ? 2 : 0;
+            if constexpr (s < NS - 1 && slot % SP == OFF && slot / SP < PER)
+                issue(min(kt + NST - 1, KT - 1), IC<j + NST - 1>{}, IC<slot / SP>{});
             __builtin_amdgcn_sched_barrier(0);
         });
         frag_wait(IC<st ^ 1>{});
@@ -249,7 +259,7 @@ __global__ __launch_bounds__(256, 1) void k_gemm_f32r(GemmArgs g)
                 slice(kt, J, IC<0>{});
                 slice(kt, J, IC<1>{});
                 slice(kt, J, IC<2>{});
-                ring_wait<2 * PER>();  // this wave's loads of step kt + 1 landed
+                ring_wait<(NST - 2) * PER>();  // this wave's loads of step kt + 1 landed
                 ring_barrier();        // ... everyone's; step kt's stage is free
                 slice(kt, J, IC<3>{});
             }
@@ -302,16 +312,21 @@ bool gemm_f32r_eligible(const GemmArgs &g, bool a_kc, bool b_kc)
            (b_kc ? (g.b_sk == 1 && g.b_sn <= kMaxPitch) : (g.b_sn == 1 && g.b_sk <= kMaxPitch && g.N % 4 == 0 && g.N >= 4));
 }
 
-void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, hipStream_t s)
+void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, int stages, hipStream_t s)
 {
     const dim3 grid((unsigned)((long long)g.tiles_m * g.tiles_n * g.batch), (unsigned)(g.ksplit > 1 ? g.ksplit : 1));
-    if (a_kc) {
-        if (b_kc) k_gemm_f32r<true, true><<<grid, 256, 0, s>>>(g);
-        else k_gemm_f32r<true, false><<<grid, 256, 0, s>>>(g);
-    } else {
-        if (b_kc) k_gemm_f32r<false, true><<<grid, 256, 0, s>>>(g);
-        else k_gemm_f32r<false, false><<<grid, 256, 0, s>>>(g);
-    }
+    auto go = [&](auto NSTC) {
+        constexpr int NST = decltype(NSTC)::value;
+        if (a_kc) {
+            if (b_kc) k_gemm_f32r<true, true, NST><<<grid, 256, 0, s>>>(g);
+            else k_gemm_f32r<true, false, NST><<<grid, 256, 0, s>>>(g);
+        } else {
+            if (b_kc) k_gemm_f32r<false, true, NST><<<grid, 256, 0, s>>>(g);
+            else k_gemm_f32r<false, false, NST><<<grid, 256, 0, s>>>(g);
+        }
+    };
+    if (stages == 2) go(IC<2>{});
+    else go(IC<4>{});
 }
 
 }  // namespace pt

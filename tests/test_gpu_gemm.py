@@ -207,6 +207,22 @@ def test_matmul_fp32_ring(A, bmnk, layout):
         A.load().pt_matmul_set_tile(-1)
 
 
+def test_matmul_fp32_ring_two_stages():
+    """The ring kernel's 2-stage form (64 KiB of LDS, two workgroups per CU,
+    every load of a step landed at its barrier), selected for whole and
+    split-K products by PT_F32R_STAGES / PT_F32R_SPLIT_STAGES, which are read
+    once per process: the fp32 ring cases above in a child process."""
+    import subprocess
+    import sys
+    env = dict(os.environ, PT_F32R_STAGES="2", PT_F32R_SPLIT_STAGES="2")
+    proc = subprocess.run([sys.executable, "-m", "pytest", os.path.abspath(__file__), "-q", "-x",
+                           "-p", "no:cacheprovider", "-k", "test_matmul_fp32_ring and not two_stages"],
+                          capture_output=True, text=True, timeout=600, env=env,
+                          cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    assert proc.returncode == 0, proc.stdout[-3000:] + proc.stderr[-2000:]
+    assert " passed" in proc.stdout and "failed" not in proc.stdout
+
+
 @pytest.mark.parametrize("dt", [O.BF16, O.F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN"])
 @pytest.mark.parametrize("bmnk", [(1, 512, 256, 512), (2, 256, 512, 128), (3, 256, 256, 64),
