@@ -47,9 +47,9 @@ HBM_PEAK_GBS = 8000.0
 # Re-measured when a kernel changes.
 PMC_TRAFFIC_BYTES = {
     "reduce:sum": 134_491_134, "reduce:mean": 134_492_158, "reduce:max": 134_492_158,
-    "reduce:argmax": 134_496_253, "reduce:var": 134_526_968, "reduce:softmax": 268_507_123,
-    "reduce:layernorm": 269_116_425, "fused:tanh_x_plus_y_z": 1_610_491_925,
-    "gemm:bf16": 1_076_311_046, "gemm:fp16": 1_086_794_548, "gemm:fp32": 2_147_509_052,
+    "reduce:argmax": 134_496_253, "reduce:var": 134_521_849, "reduce:softmax": 268_487_671,
+    "reduce:layernorm": 269_103_243, "fused:tanh_x_plus_y_z": 1_610_491_925,
+    "gemm:bf16": 1_073_920_169, "gemm:fp16": 1_088_352_095, "gemm:fp32": 3_757_844_716,
 }
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
 # pt_backend_info last_matmul path -> kernel symbol

@@ -1753,16 +1753,53 @@ static bool run_steps(Plan &p, std::vector<TensorP> &vals)
     return true;
 }
 
-// Graph capture over several streams.  Each step runs on a branch: the
-// branch of its latest dependency when that branch has not moved on, else
-// the least recently used branch, after waiting on the events of the steps
-// it reads that ran on other branches.  Independent steps (the weight and
-// input gradients of one layer, a bias-gradient reduction beside a GEMM,
-// the optimizer update of one layer beside the next layer's products) then
-// become parallel branches of the captured graph, as the reference's plan
-// stream orders native and fused steps (fusion_execute.c:385-412); the
-// values and the order of every dependency are unchanged.
+// Graph capture over several streams.  Each step runs on a branch, after
+// waiting on the events of the steps it reads that ran on other branches.
+// Independent steps (the weight and input gradients of one layer, a
+// bias-gradient reduction beside a GEMM, the optimizer update of one layer
+// beside the next layer's products) then become parallel branches of the
+// captured graph, as the reference's plan stream orders native and fused
+// steps (fusion_execute.c:385-412); the values and the order of every
+// dependency are unchanged.  The branch is chosen on estimated times (a
+// list schedule): the one where the step could start first, preferring the
+// branch of its latest dependency when that branch has not moved on (no
+// cross-branch wait), then the least recently used one.  A product that
+// fills the device queues behind the previous such product whatever its
+// branch, so a short step is not placed behind a product it does not need:
+// in the config-5 step the first layer's bias-gradient sum and its update
+// ran after the second layer's weight gradient on one branch, 19 us after
+// the last product.
 static constexpr int kBranches = 3;
+
+// Rough duration of a step in microseconds, for branch placement only:
+// products at 120 TFLOP/s, other steps at 6 TB/s of what they read and
+// write, plus 3 us per launch.  `heavy`: a product of at least 2 GFLOP,
+// which holds every CU while it runs.
+static double step_cost_us(const Plan &p, const Step &st, bool &heavy)
+{
+    heavy = false;
+    auto bytes_of = [&](int id) {
+        const TensorP &t = p.items[id].t;
+        return (double)t->numel() * (double)dtype_size(t->dtype);
+    };
+    if (st.native) {
+        const Item &it = p.items[st.item];
+        if (it.t->node->native.kind == 0 && it.args.size() == 2) {  // matmul
+            const TensorP &a = p.items[it.args[0]].t;
+            const double flops = 2.0 * (double)it.t->numel() * (double)a->shape[a->ndims - 1];
+            heavy = flops >= 2e9;
+            return 3.0 + flops / 120e6;
+        }
+        double b = bytes_of(st.item);
+        for (int a : it.args) b += bytes_of(a);
+        return 3.0 + b / 6e6;
+    }
+    const Kernel &k = p.kernels[st.kernel];
+    double b = 0;
+    for (int l : k.leaves) b += bytes_of(l);
+    for (int r : k.roots) b += bytes_of(r);
+    return 3.0 + b / 6e6;
+}
 
 // The side streams of the branches (this thread's), created outside any
 // graph capture.
@@ -1813,6 +1850,10 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
     std::vector<char> joined(kBranches, 0);
     joined[0] = 1;
     std::vector<pt_event_t> done(ns, nullptr);
+    // estimated end of each step, of each branch's queued work and of the
+    // last device-filling product
+    std::vector<double> est_end(ns, 0.0), free_at(kBranches, 0.0);
+    double device_free = 0.0;
     for (int i = 0; i < ns && ok; i++) {
         const Step &st = p.steps[i];
         const int chain = chain_of(p, i);
@@ -1825,20 +1866,42 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
                 for (int l : p.kernels[s.kernel].leaves) deps.push_back(producer[l]);
             }
         };
-        if (chain >= 0)
-            for (int m : p.chains[chain].members) step_deps(p.steps[m]);
-        else
+        double cost = 0.0;
+        bool heavy = false;
+        if (chain >= 0) {
+            for (int m : p.chains[chain].members) {
+                step_deps(p.steps[m]);
+                bool h = false;
+                cost += step_cost_us(p, p.steps[m], h);
+            }
+        } else {
             step_deps(st);
+            cost = step_cost_us(p, st, heavy);
+        }
         deps.erase(std::remove(deps.begin(), deps.end(), -1), deps.end());
         deps.erase(std::remove(deps.begin(), deps.end(), i), deps.end());
-        int latest = deps.empty() ? -1 : *std::max_element(deps.begin(), deps.end());
-        int b = -1;
-        if (latest >= 0 && last[branch[latest]] == latest) b = branch[latest];
-        if (b < 0) {
-            b = 0;
-            for (int c = 1; c < kBranches; c++)
-                if (last[c] < last[b]) b = c;
+        const int latest = deps.empty() ? -1 : *std::max_element(deps.begin(), deps.end());
+        double ready = 0.0;
+        for (int d : deps) ready = std::max(ready, est_end[d]);
+        const int stay = latest >= 0 && last[branch[latest]] == latest ? branch[latest] : -1;
+        auto start_on = [&](int c) {
+            const double t = std::max(ready, free_at[c]);
+            return heavy ? std::max(t, device_free) : t;
+        };
+        int b = stay;
+        for (int c = 0; c < kBranches; c++) {
+            if (b < 0) {
+                b = c;
+                continue;
+            }
+            const double sc = start_on(c), sb = start_on(b);
+            // earlier start; on a tie keep the dependency's branch, else
+            // the least recently used
+            if (sc < sb - 1e-9 || (sc <= sb + 1e-9 && b != stay && last[c] < last[b])) b = c;
         }
+        est_end[i] = start_on(b) + cost;
+        free_at[b] = est_end[i];
+        if (heavy) device_free = est_end[i];
         if (!joined[b]) {
             ok = check_status(pt_stream_wait_event(streams[b], fork), "Fusion branch join");
             joined[b] = 1;
