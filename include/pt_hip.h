@@ -263,14 +263,18 @@ const char *pt_matmul_precision_name(void);
 
 /* Tile override for the MFMA kernels, the tuning knob that replaces
  * cuda_blas_tune_matmul (matmul_kernels.h:34-38): 0 = 256x128, 1 = 128x128,
- * 2 = 64x64, 3 = 256x256 workgroup tiles, 4 / 5 = 256x128 / 256x256 with a
- * doubled K step, 6 / 7 = 256x256 with 4 waves (single / doubled K step),
- * 8 = 256x256 direct-to-LDS kernel for f16/bf16 (whole tiles, K a multiple
- * of 64, k-contiguous A; other cases run tile 3), 9 = 256x128 with 8 waves
- * (the large-problem fp32 choice), 10 / 11 = 128x128 with 8 waves (single /
- * doubled K step), 12 / 13 = 128x64 with 4 waves and two workgroups per CU
- * (single / doubled K step; the mid-size fp32 choice); 11-13 are fp32 only
- * and 16-bit requests run 128x128.  -1 = automatic choice (default). */
+ * 2 = 64x64, 3 = 256x256 workgroup tiles, 5 = 256x256 with a doubled K step
+ * (4, 6 and 7 are not built and are refused), 8 = 256x256 direct-to-LDS
+ * kernel for f16/bf16 (whole tiles, K a multiple of 64, k-contiguous A;
+ * other cases run tile 3), 9 = 256x128 with 8 waves, 10 / 11 = 128x128 with
+ * 8 waves (single / doubled K step), 12 / 13 = 128x64 with 4 waves and two
+ * workgroups per CU (single / doubled K step); 11-13 are fp32 only and
+ * 16-bit requests run 128x128.  14-37 = the 16-bit LDS-ring kernels (37, the
+ * whole-line ring, is the default for large bf16/fp16 products), 38 = the
+ * fp32 LDS-ring kernel (128x128 tiles), the default for fp32 products of
+ * 128x128 tiles and up whose operands come in 16-byte packs and whose K is
+ * a multiple of 32 (others run tile 10; 16-bit requests run 128x128).
+ * -1 = automatic choice (default). */
 pt_status pt_matmul_set_tile(int tile);
 /* Measured tile choice for one problem, the counterpart of
  * cuda_blas_tune_matmul (matmul_kernels.h:34-38; a cuBLASLt candidate sweep
