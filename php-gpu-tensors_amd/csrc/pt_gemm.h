@@ -141,15 +141,18 @@ __device__ __forceinline__ void lds_read_b128(T &dst, uint32_t addr)
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF));
 }
 // One load of 16 bytes per lane into LDS: the wave-uniform base address in
-// a scalar raw-buffer resource (stride 0, no range limit), the lane's byte
-// offset in a register, the LDS destination (wave-uniform) in M0.  Unlike
+// a scalar raw-buffer resource (stride 0), the lane's byte offset in a
+// register, the LDS destination (wave-uniform) in M0.  Unlike
 // global_load_lds with a per-lane 64-bit address, a load then needs no
-// vector instruction of its own.
-__device__ __forceinline__ void buffer_load_lds16(const void *base, uint32_t lane_off, PT_LDS_AS void *lds)
+// vector instruction of its own.  `range`: bytes from `base` that may be
+// read; the buffer unit returns zeros for a lane's bytes past it instead of
+// reading them.
+__device__ __forceinline__ void buffer_load_lds16(const void *base, uint32_t lane_off, PT_LDS_AS void *lds,
+                                                  uint32_t range = 0xffffffffu)
 {
     constexpr int kRsrcWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format
     const __amdgpu_buffer_rsrc_t r =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, -1, kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)range, kRsrcWord3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, lane_off, 0, 0, 0);
 }
 

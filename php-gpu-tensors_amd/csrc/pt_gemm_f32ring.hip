@@ -48,9 +48,11 @@ namespace pt {
 //     workgroup's waves keep the SIMD busy while these wait.
 // Fragments of slice s + 1 are read while slice s runs on the matrix cores.
 // Edge tiles: rows past M (columns past N) load the last whole row or
-// 16-byte pack instead and are not stored.  K steps must be whole (each K
-// chunk a multiple of 32).
-template <bool A_KC, bool B_KC, int NST>
+// 16-byte pack instead and are not stored.  K must be a multiple of 16: a K
+// chunk that ends half-way through its last 32-k step reads that step's
+// loads within the operand's extent (the buffer resource's range) and zeroes
+// both operands' fragments of its last two 8-k slices.
+template <bool A_KC, bool B_KC, int NST, bool TAIL>
 __global__ __launch_bounds__(256, NST == 2 ? 2 : 1) void k_gemm_f32r(GemmArgs g)
 {
     constexpr int BM = 128, BN = 128, BK = 32, NS = BK / 8;
@@ -124,18 +126,43 @@ __global__ __launch_bounds__(256, NST == 2 ? 2 : 1) void k_gemm_f32r(GemmArgs g)
     const char *B0 = (const char *)(B + (B_KC ? (long long)n0 * g.b_sn : (long long)n0));
     const long long sta = (A_KC ? (long long)BK : (long long)BK * g.a_sk) * 4;
     const long long stb = (B_KC ? (long long)BK : (long long)BK * g.b_sk) * 4;
-    const int KT = Kl / BK;
+    // a K chunk may end half-way through its last 32-k step (K a multiple
+    // of 16): that step's loads reach 16 k past the chunk, and the loads of
+    // each step may read only up to the operand's last element (the buffer
+    // unit returns zeros past it)
+    const int KT = (Kl + BK - 1) / BK;
+    // TAIL (K not a multiple of 32): the step whose upper half lies past
+    // the chunk (-1: none), compared as a uniform integer so that the check
+    // stays a scalar branch.  Without TAIL the kernel has neither this check
+    // nor the range limit, which cost its loop 1.1 % on 4096 x 1024 x 4096.
+    const int half_step = TAIL && (Kl % BK) != 0 ? KT - 1 : -1;
+    const char *endA = (const char *)((const float *)g.a + oa +
+                                      (long long)(g.M - 1) * g.a_sm + (long long)(g.K - 1) * g.a_sk + 1);
+    const char *endB = (const char *)((const float *)g.b + ob +
+                                      (long long)(g.N - 1) * g.b_sn + (long long)(g.K - 1) * g.b_sk + 1);
+    auto range_to = [](const char *base, const char *end) {
+        const long long r = end - base;
+        return (uint32_t)(r <= 0 ? 0 : (r >= 0xffffffffLL ? 0xffffffffLL : r));
+    };
+    // only the last step can reach past an operand (earlier steps end
+    // within the chunk, and rows and columns are clamped): its range is
+    // computed once, and a step picks it with a scalar compare
+    const uint32_t last_a = range_to(A0 + (long long)(KT - 1) * sta, endA);
+    const uint32_t last_b = range_to(B0 + (long long)(KT - 1) * stb, endB);
 
     // load IDX of step kt into stage J (loads past the last step re-read it:
     // in bounds, never consumed, and every step waits for the same count)
     auto issue = [&](int kt, auto J, auto IDX) {
         constexpr int j = decltype(J)::value % NST, q = decltype(IDX)::value;
         if constexpr (q < NQ) {
-            buffer_load_lds16(A0 + (long long)kt * sta, offa[q], (PT_LDS_AS void *)(lds_a + j * SE + (wave * NQ + q) * 256));
+            buffer_load_lds16(A0 + (long long)kt * sta, offa[q],
+                              (PT_LDS_AS void *)(lds_a + j * SE + (wave * NQ + q) * 256),
+                              TAIL && kt >= KT - 1 ? last_a : 0xffffffffu);
         } else {
             constexpr int q2 = q - NQ;
             buffer_load_lds16(B0 + (long long)kt * stb, offb[q2],
-                              (PT_LDS_AS void *)(lds_b + j * SE + (wave * NQ + q2) * 256));
+                              (PT_LDS_AS void *)(lds_b + j * SE + (wave * NQ + q2) * 256),
+                              TAIL && kt >= KT - 1 ? last_b : 0xffffffffu);
         }
     };
 
@@ -224,6 +251,23 @@ __global__ __launch_bounds__(256, NST == 2 ? 2 : 1) void k_gemm_f32r(GemmArgs g)
     // slices 0-2, the loads of step kt + 3
     auto slice = [&](int kt, auto J, auto S) {
         constexpr int j = decltype(J)::value, s = decltype(S)::value, st = s & 1;
+        if constexpr (TAIL && s >= 2) {
+            // k 16..31 of a half step past the chunk's end: both operands'
+            // fragments are zeroed, so these MFMAs add exact zeros whatever
+            // the loads brought (the next row's values, or zeros)
+            if (kt == half_step) {
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    if constexpr (A_KC) fak[st][i] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
+                    if constexpr (B_KC) fbk[st][i] = (floatx4){0.0f, 0.0f, 0.0f, 0.0f};
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    if constexpr (!A_KC) fam[st][e] = (f32x2v_t){0.0f, 0.0f};
+                    if constexpr (!B_KC) fbm[st][e] = (f32x2v_t){0.0f, 0.0f};
+                }
+            }
+        }
         static_for<0, 16>([&](auto Q) {
             constexpr int q = decltype(Q)::value;
             mfma_one(IC<st>{}, Q);
@@ -303,11 +347,12 @@ bool gemm_f32r_eligible(const GemmArgs &g, bool a_kc, bool b_kc)
 {
     // 16-byte packs along each operand's contiguous dimension (vec_a /
     // vec_b: contiguous stride 1, pitch and batch offsets multiples of 4,
-    // aligned base), whole K steps, for an m- or n-contiguous operand a
+    // aligned base), K a multiple of 16 (a last half step of 32 is
+    // zero-filled; split chunks are whole steps), for an m- or n-contiguous operand a
     // whole last pack to clamp edge loads to, and pitches that keep a lane's
     // byte offset within a step (at most 127 pitches) in 32 bits
     constexpr long long kMaxPitch = 1LL << 22;
-    return g.vec_a && g.vec_b && g.K % 32 == 0 && (g.ksplit <= 1 || g.k_chunk % 32 == 0) &&
+    return g.vec_a && g.vec_b && g.K % 16 == 0 && (g.ksplit <= 1 || g.k_chunk % 32 == 0) &&
            (a_kc ? (g.a_sk == 1 && g.a_sm <= kMaxPitch) : (g.a_sm == 1 && g.a_sk <= kMaxPitch && g.M % 4 == 0 && g.M >= 4)) &&
            (b_kc ? (g.b_sk == 1 && g.b_sn <= kMaxPitch) : (g.b_sn == 1 && g.b_sk <= kMaxPitch && g.N % 4 == 0 && g.N >= 4));
 }
@@ -315,18 +360,21 @@ bool gemm_f32r_eligible(const GemmArgs &g, bool a_kc, bool b_kc)
 void launch_gemm_f32r(const GemmArgs &g, bool a_kc, bool b_kc, int stages, hipStream_t s)
 {
     const dim3 grid((unsigned)((long long)g.tiles_m * g.tiles_n * g.batch), (unsigned)(g.ksplit > 1 ? g.ksplit : 1));
-    auto go = [&](auto NSTC) {
+    auto go = [&](auto NSTC, auto TAILC) {
         constexpr int NST = decltype(NSTC)::value;
+        constexpr bool TAIL = decltype(TAILC)::value != 0;
         if (a_kc) {
-            if (b_kc) k_gemm_f32r<true, true, NST><<<grid, 256, 0, s>>>(g);
-            else k_gemm_f32r<true, false, NST><<<grid, 256, 0, s>>>(g);
+            if (b_kc) k_gemm_f32r<true, true, NST, TAIL><<<grid, 256, 0, s>>>(g);
+            else k_gemm_f32r<true, false, NST, TAIL><<<grid, 256, 0, s>>>(g);
         } else {
-            if (b_kc) k_gemm_f32r<false, true, NST><<<grid, 256, 0, s>>>(g);
-            else k_gemm_f32r<false, false, NST><<<grid, 256, 0, s>>>(g);
+            if (b_kc) k_gemm_f32r<false, true, NST, TAIL><<<grid, 256, 0, s>>>(g);
+            else k_gemm_f32r<false, false, NST, TAIL><<<grid, 256, 0, s>>>(g);
         }
     };
-    if (stages == 2) go(IC<2>{});
-    else go(IC<4>{});
+    // a K that ends half-way through a 32-k step runs the 4-stage tail form
+    if (g.K % 32 != 0) go(IC<4>{}, IC<1>{});
+    else if (stages == 2) go(IC<2>{}, IC<0>{});
+    else go(IC<4>{}, IC<0>{});
 }
 
 }  // namespace pt

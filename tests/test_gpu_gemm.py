@@ -153,25 +153,30 @@ def test_matmul_split_k(A, bmnk, dt):
 
 def _ring_eligible(m, n, k, layout):
     """The fp32 ring kernel's conditions (pt_gemm_f32ring.hip) for these
-    aligned, packed operands: whole K steps of 32, and a transposed (m- or
-    n-contiguous) operand needs its M or N a multiple of 4."""
+    aligned, packed operands: K a multiple of 16 (a last half step of 32 is
+    zero-filled), and a transposed (m- or n-contiguous) operand needs its M
+    or N a multiple of 4."""
     a_rc, b_rc = layout[0] == "T", layout[1] == "N"
-    return k % 32 == 0 and (not a_rc or m % 4 == 0) and (not b_rc or n % 4 == 0)
+    return k % 16 == 0 and (not a_rc or m % 4 == 0) and (not b_rc or n % 4 == 0)
 
 
 @pytest.mark.parametrize("layout", ["NN", "NT", "TN", "TT"])
 @pytest.mark.parametrize("bmnk", [(2, 256, 384, 128), (1, 300, 260, 96), (1, 784, 1024, 4096),
                                   (3, 130, 258, 64), (1, 128, 129, 32), (1, 1024, 1024, 2048),
-                                  (2, 256, 256, 130)], ids=str)
+                                  (2, 256, 256, 130), (1, 512, 1024, 784), (2, 132, 260, 16),
+                                  (1, 1024, 1024, 2064), (1, 300, 260, 80)], ids=str)
 def test_matmul_fp32_ring(A, bmnk, layout):
     """Tile 38, the fp32 LDS-ring kernel: every operand layout (A k- or
     m-contiguous, B n- or k-contiguous), whole and edge tiles (rows past M
     and columns past N load clamped packs and are not stored), batches, and
-    split-K over long K with few tiles.  Integer-valued operands keep every
-    sum exact, so outputs are bit-exact against numpy's float64 product.
-    Shapes the kernel does not take (K % 32 != 0, a transposed operand whose
-    M or N is not a multiple of 4) run the 8-wave 128x128 kernel instead and
-    must agree too."""
+    split-K over long K with few tiles, and K ending half-way through a
+    32-k step (784, 80, 16; 2064 split four ways, whose last chunk ends so),
+    where the loads past the operand's end read zeros and the half step's
+    upper slices are zeroed.  Integer-valued operands keep every sum exact,
+    so outputs are bit-exact against numpy's float64 product.  Shapes the
+    kernel does not take (K % 16 != 0, a transposed operand whose M or N is
+    not a multiple of 4) run the 8-wave 128x128 kernel instead and must
+    agree too."""
     from phptensors import synthetic
     b_, m, n, k = bmnk
     A.load().pt_matmul_set_tile(38)
