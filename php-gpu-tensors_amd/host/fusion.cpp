@@ -1916,12 +1916,16 @@ static bool run_steps_branched(Plan &p, std::vector<TensorP> &vals, std::vector<
         pt_stream_set_current(nullptr);
         if (ok) ok = new_event(done[i]) && check_status(pt_event_record(done[i], streams[b]), "Fusion branch event");
     }
-    // every branch joins the capture stream again before the capture ends
-    for (int b = 1; b < kBranches && ok; b++) {
+    // every branch joins the capture stream again before the capture ends,
+    // also after a failure: a capture ended with a side stream still joined
+    // to it leaves that stream capturing, and later allocations and frees
+    // on the device then fail or crash
+    for (int b = 1; b < kBranches; b++) {
         if (!joined[b]) continue;
         pt_event_t e = nullptr;
-        ok = new_event(e) && check_status(pt_event_record(e, streams[b]), "Fusion branch end") &&
-             check_status(pt_stream_wait_event(streams[0], e), "Fusion branch end");
+        const bool joined_ok = new_event(e) && check_status(pt_event_record(e, streams[b]), "Fusion branch end") &&
+                               check_status(pt_stream_wait_event(streams[0], e), "Fusion branch end");
+        ok = ok && joined_ok;
     }
     return ok;
 }
