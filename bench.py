@@ -307,7 +307,7 @@ def gemm_cpu_baseline():
     """Oracle matmul (the HostArray restatement: one sequential fmaf sum per
     output, contiguous_array_ce.c:1295-1343) on one whole batch of config 4,
     its outputs split over the host threads; the 32 batches take 32 times as
-    long (BASELINE.md's CPU plan)."""
+    long."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
     m = k = n = 2048
